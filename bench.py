@@ -1,0 +1,294 @@
+"""Benchmark of the MI355X quantized implicit-GEMM conv path (BASELINE.json's metric).
+
+``python bench.py [--steps K] [--warmup W]`` prints ONE JSON line. The headline workload is BASELINE config 2 (the
+MXFP8 1x1 conv, N=2, 100x100, 512 -> 512, fused bias + GELU, BF16 out): a "step" is one launch of the implicit-GEMM
+conv on E4M3 activations already resident in HBM. ``value`` is its throughput in TOPS (dense MXFP8 operations:
+2 * M * N * K per launch); ``roofline`` relates the same launch to the HBM roofline (config 2's arithmetic intensity,
+338 FLOP/B, is below the MI355X ridge of 625 FLOP/B). ``configs`` reports every BASELINE config on the same run:
+per-kernel ms, TOPS or GB/s and roofline fractions, and the refiner block / stack ms.
+
+Timing: each measured launch sequence is captured once in a HIP graph and replayed; K replays are bracketed by
+``torch.cuda.synchronize()`` and HIP events on the stream the kernels run on (torch's current stream); the
+per-launch time is the event time divided by the launches. ``cpu_baseline`` times this repository's torch CPU oracle of
+the same op (FlashIM's reference path restated) on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+METRIC = "TOPS + % MFMA peak, MXFP8/INT8 implicit-GEMM conv; ms per refiner stack"
+PEAK_MX_TFLOPS = 5000.0  # dense MXFP8 / FP8 MFMA, MI355X
+PEAK_INT8_TOPS = 5000.0  # dense INT8 MFMA
+PEAK_HBM_GBS = 8000.0
+DEV = "cuda"
+
+
+def parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--only", default=None, help="run one workload only (cfg1|cfg2|cfg3|cfg3q|cfg4|cfg5int8|cfg5mxfp8|copy)"
+                                                  " and print its line (profiling runs)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-stack", action="store_true", help="skip configs 4 and 5")
+    return p.parse_args()
+
+
+# -- timing ----------------------------------------------------------------------------------------------------
+
+
+def time_graph(fn, steps: int, warmup: int, launches: int = 1) -> float:
+    """Mean ms per replay of ``fn`` captured as a HIP graph (``launches`` kernels per replay)."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def time_cpu(fn, budget_s: float = 10.0, max_calls: int = 50, warmup: int = 2) -> tuple[float, int]:
+    """Median ms of ``fn`` over up to ``max_calls`` calls within ``budget_s`` seconds (after ``warmup`` calls)."""
+    for _ in range(warmup):
+        fn()
+    samples = []
+    t_end = time.perf_counter() + budget_s
+    while len(samples) < max_calls and (not samples or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        fn()
+        samples.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(samples), len(samples)
+
+
+# -- workloads -------------------------------------------------------------------------------------------------
+
+
+def cfg1():
+    """INT8 3x3 conv, NHWC N=1, 128x128, 64 -> 64, stride 1, pad 1; per-tensor activation scale, per-channel int8
+    weights, fp32 bias."""
+    from flashim_amd import ops, quant
+
+    g = torch.Generator(device="cpu").manual_seed(1)
+    act = torch.randn(1, 64, 128, 128, generator=g).to(DEV)
+    a_scale = (act.abs().amax() / 127).float()
+    x = ops.quantize_int8(act.permute(0, 2, 3, 1), a_scale).values
+    w = (torch.randn(64, 64, 3, 3, generator=g) * 0.05).to(DEV)
+    wq, w_scale = quant.weight_scales_and_values(w.permute(0, 2, 3, 1).reshape(64, -1))
+    bias = torch.randn(64, generator=g).to(DEV)
+    args = (x, wq, a_scale, w_scale, bias, 3, 3, 1, 1, 1, 1, 1, 1)
+    fn = lambda: ops.int8_conv2d(*args)  # noqa: E731
+    m, n, k = 128 * 128, 64, 576
+    return fn, {"ops": 2 * m * n * k, "bytes": m * 64 + n * k + 4 * n + m * n * 2, "kind": "int8"}, args
+
+
+def _mx_act(shape_nchw, g, outliers: bool):
+    x = torch.randn(*shape_nchw, generator=g)
+    if outliers:
+        c = shape_nchw[1]
+        factor = torch.exp(torch.empty(c).uniform_(math.log(0.1), math.log(10.0), generator=g))
+        x = x * factor[None, :, None, None]
+    return x.to(torch.bfloat16).to(DEV).permute(0, 2, 3, 1).contiguous()
+
+
+def cfg2():
+    """MXFP8 1x1 conv, NHWC N=2, 100x100, 512 -> 512; outlier-channel activations; bias + GELU; BF16 out."""
+    from flashim_amd import ops, quant
+
+    g = torch.Generator(device="cpu").manual_seed(2)
+    x_bf16 = _mx_act((2, 512, 100, 100), g, outliers=True)
+    exponent = quant.calibrate_block32_exponent(x_bf16)
+    xq = ops.quantize_mxfp8(x_bf16, exponent).values
+    w = quant.QuantizedWeight.from_float((torch.randn(512, 512, generator=g) * 0.05).to(DEV))
+    bias = (torch.randn(512, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+    args = (xq, exponent, w.values, w.scale_exponent, bias, 1, 1, 1, 1, 0, 0, 1, 1)
+    fn = lambda: ops.mxfp8_conv2d(*args, gelu=True)  # noqa: E731
+    m, n, k = 20000, 512, 512
+    nbytes = m * k + n * k + n * k // 32 + 2 * n + m * n * 2
+    return fn, {"ops": 2 * m * n * k, "bytes": nbytes, "kind": "mxfp8"}, args
+
+
+def cfg3():
+    """MXFP8 3x3 conv, NHWC N=2, 200x200, 128 -> 128, pad 1; weights N(0, 0.03) with a folded BatchNorm affine;
+    bias + ReLU epilogue; BF16 out. Returns the conv and, separately, the activation quantizer."""
+    from flashim_amd import ops, quant
+
+    g = torch.Generator(device="cpu").manual_seed(3)
+    x_bf16 = _mx_act((2, 128, 200, 200), g, outliers=False)
+    exponent = quant.calibrate_block32_exponent(x_bf16)
+    w = torch.randn(128, 128, 3, 3, generator=g) * 0.03
+    gamma, beta = torch.rand(128, generator=g) + 0.5, torch.randn(128, generator=g) * 0.1
+    mean, var = torch.randn(128, generator=g) * 0.1, torch.rand(128, generator=g) + 0.5
+    inv = gamma / torch.sqrt(var + 1e-5)
+    w_folded = w * inv[:, None, None, None]
+    b_folded = beta - mean * inv
+    wq = quant.QuantizedWeight.from_float(w_folded.permute(0, 2, 3, 1).reshape(128, -1).to(DEV))
+    bias = b_folded.to(torch.bfloat16).to(DEV)
+    xq = ops.quantize_mxfp8(x_bf16, exponent).values
+    args = (xq, exponent, wq.values, wq.scale_exponent, bias, 3, 3, 1, 1, 1, 1, 1, 1)
+    conv = lambda: ops.mxfp8_conv2d(*args, relu=True)  # noqa: E731
+    quantize = lambda: ops.quantize_mxfp8(x_bf16, exponent)  # noqa: E731
+    m, n, k = 80000, 128, 1152
+    conv_bytes = m * 128 + n * k + n * k // 32 + 2 * n + m * n * 2
+    q_bytes = m * 128 * 2 + m * 128
+    return (conv, {"ops": 2 * m * n * k, "bytes": conv_bytes, "kind": "mxfp8"}, args), \
+        (quantize, {"bytes": q_bytes}, (x_bf16, exponent))
+
+
+def copy_calibration():
+    """A plain device copy of a known size (the PMC traffic calibration)."""
+    src = torch.empty(64 << 20, device=DEV, dtype=torch.uint8).fill_(1)
+    dst = torch.empty_like(src)
+    return lambda: dst.copy_(src), src.numel()
+
+
+# -- CPU baseline (oracle) ---------------------------------------------------------------------------------------
+
+
+def cpu_baseline_cfg2(args, steps_budget_s: float = 10.0) -> dict:
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import reference as ref
+
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    cpu_args = [a.cpu() if isinstance(a, torch.Tensor) else a for a in args]
+    ms, calls = time_cpu(lambda: ref.mxfp8_conv2d(*cpu_args, gelu=True), budget_s=steps_budget_s)
+    ops = 2 * 20000 * 512 * 512
+    return {
+        "value": round(ops / (ms * 1e-3) / 1e12, 5), "unit": "TOPS", "cores": cores, "kind": "port",
+        "ms": round(ms, 3),
+        "sample": f"config 2 in full (M=20000, K=N=512, bias+GELU): oracle.reference.mxfp8_conv2d (torch CPU, "
+                  f"FlashIM's reference path restated), median of {calls} calls, torch threads={cores}",
+    }
+
+
+# -- main --------------------------------------------------------------------------------------------------------
+
+
+def main() -> int:
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {a.gpus}).",
+              file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    torch.backends.cuda.matmul.allow_tf32 = False
+    steps, warmup = a.steps, a.warmup
+
+    if a.only == "copy":
+        fn, nbytes = copy_calibration()
+        ms = time_graph(fn, steps, warmup)
+        print(json.dumps({"workload": "copy", "bytes": nbytes, "ms": ms, "GBps": 2 * nbytes / ms / 1e6}))
+        return 0
+
+    results = {}
+
+    def gemm_line(name, fn, info):
+        ms = time_graph(fn, steps, warmup)
+        peak = PEAK_INT8_TOPS if info["kind"] == "int8" else PEAK_MX_TFLOPS
+        tops = info["ops"] / (ms * 1e-3) / 1e12
+        gbs = info["bytes"] / (ms * 1e-3) / 1e9
+        ai = info["ops"] / info["bytes"]
+        attainable = min(peak, ai * PEAK_HBM_GBS / 1e3)
+        results[name] = {
+            "ms": round(ms, 5), "TOPS": round(tops, 2), "mfma_peak_frac": round(tops / peak, 4),
+            "GBps": round(gbs, 1), "AI": round(ai, 1), "attainable_TOPS": round(attainable, 1),
+            "roofline_frac": round(tops / attainable, 4), "bound": "mfma" if ai * PEAK_HBM_GBS / 1e3 >= peak else "hbm",
+        }
+        return ms
+
+    def hbm_line(name, fn, info):
+        ms = time_graph(fn, steps, warmup)
+        gbs = info["bytes"] / (ms * 1e-3) / 1e9
+        results[name] = {"ms": round(ms, 5), "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)}
+        return ms
+
+    only = a.only
+    c2 = None
+    if only in (None, "cfg1"):
+        fn, info, _ = cfg1()
+        gemm_line("cfg1_int8_3x3", fn, info)
+    if only in (None, "cfg2"):
+        fn, info, c2_args = cfg2()
+        c2 = (fn, info, c2_args)
+        gemm_line("cfg2_mxfp8_1x1_gelu", fn, info)
+    if only in (None, "cfg3", "cfg3q"):
+        (conv, cinfo, _), (qfn, qinfo, _) = cfg3()
+        if only in (None, "cfg3"):
+            gemm_line("cfg3_mxfp8_3x3_bn_relu", conv, cinfo)
+        if only in (None, "cfg3q"):
+            hbm_line("cfg3q_quantize_mxfp8", qfn, qinfo)
+    if not a.no_stack and only in (None, "cfg4", "cfg5int8", "cfg5mxfp8"):
+        from flashim_amd import blocks
+
+        if only in (None, "cfg4"):
+            for preset in ("mxfp8", "int8"):
+                fn, info = blocks.bench_block(preset, device=DEV)
+                ms = time_graph(fn, steps, warmup)
+                results[f"cfg4_block_{preset}"] = {
+                    "ms": round(ms, 5), "GBps_unfused_chain": round(info["bytes"] / (ms * 1e-3) / 1e9, 1),
+                    "hbm_frac": round(info["bytes"] / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                    "TOPS": round(info["ops"] / (ms * 1e-3) / 1e12, 2),
+                }
+        for preset in ("int8", "mxfp8"):
+            if only in (None, f"cfg5{preset}"):
+                fn, info = blocks.bench_stack(preset, device=DEV)
+                ms = time_graph(fn, max(3, steps // 10), max(1, warmup // 5))
+                results[f"cfg5_stack_{preset}"] = {
+                    "ms": round(ms, 4), "TOPS": round(info["ops"] / (ms * 1e-3) / 1e12, 2),
+                    "blocks": info["blocks"], "pixels_per_scale": info["pixels"],
+                }
+
+    if only is not None:
+        print(json.dumps({"workload": only, "results": results}))
+        return 0
+
+    head = results["cfg2_mxfp8_1x1_gelu"]
+    fn, info, c2_args = c2
+    ms = head["ms"]
+    value = info["ops"] / (ms * 1e-3) / 1e12
+    achieved_gbs = info["bytes"] / (ms * 1e-3) / 1e9
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TOPS", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "mxfp8_e4m3", "data": "synthetic (seeded N(0,1) x per-channel log-uniform [0.1, 10]; random-init weights)",
+        "config": {"workload": "cfg2: MXFP8 1x1 conv + bias + GELU, NHWC N=2 H=W=100 Cin=Cout=512, BF16 out",
+                   "M": 20000, "N": 512, "K": 512, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "mfma_frac": round(value / PEAK_MX_TFLOPS, 4), "algorithmic_bytes": info["bytes"]},
+        "configs": results,
+    }
+    if not a.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_cfg2(c2_args)
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

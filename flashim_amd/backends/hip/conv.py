@@ -1,0 +1,198 @@
+"""HIP impls of the quantized convolution ops, with the signatures of FlashIM's torch references:
+
+* ``int8_conv2d``  (``flashim/ops/conv.py:174-206``) -> ``fim_int8_conv2d``
+* ``mxfp8_conv2d`` (``flashim/ops/conv.py:309-342``) -> ``fim_mxfp8_conv2d``
+* ``depthwise5x5_relu_mxfp8`` / ``depthwise5x5_relu_int8`` (``flashim/ops/conv.py:30-61``) -> ``fim_depthwise5x5``
+* ``depthwise5x5_gelu`` (this backend's refiner-block producer: folded BatchNorm + GELU, BF16 / static INT8 / static
+  MXFP8 out) -> ``fim_depthwise5x5``
+
+``gelu=`` on the two convs is an epilogue FlashIM's conv ops do not have: it is ``int8_linear``'s GELU
+(``flashim/ops/gemm.py:94-95``): ``F.gelu`` of the BF16 result, rounded to BF16, before the residual.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+from torch import Tensor
+
+from flashim_amd import _lib, quant
+from flashim_amd.platforms import is_gfx950
+
+
+def conv_output_size(h: int, w: int, kh: int, kw: int, sh: int, sw: int, ph: int, pw: int, dh: int, dw: int):
+    return (h + 2 * ph - dh * (kh - 1) - 1) // sh + 1, (w + 2 * pw - dw * (kw - 1) - 1) // sw + 1
+
+
+def _bias_args(bias: Tensor | None, device: torch.device) -> tuple[Tensor | None, int]:
+    if bias is None:
+        return None, 0
+    if bias.dtype not in (torch.float32, torch.bfloat16):
+        bias = bias.float()
+    bias = bias.to(device).contiguous()
+    return bias, 1 if bias.dtype == torch.bfloat16 else 0
+
+
+def _residual_args(residual: Tensor | None, device: torch.device, out_shape: tuple[int, int, int, int]):
+    """(tensor, dtype code, channels, ctypes int64[4] strides); the kernel reads ``[B, Ho, Wo, <= Cout]``."""
+    if residual is None:
+        return None, 0, 0, None
+    if residual.ndim != 4 or tuple(residual.shape[:3]) != tuple(out_shape[:3]) or residual.shape[3] > out_shape[3]:
+        raise ValueError(f"residual {tuple(residual.shape)} does not fit the output {tuple(out_shape)}")
+    if residual.device != device:
+        raise ValueError("residual must be on the output's device")
+    if residual.dtype not in (torch.float32, torch.bfloat16):
+        residual = residual.to(torch.bfloat16)
+    strides = (ctypes.c_int64 * 4)(*residual.stride())
+    return residual, _lib.DTYPE_CODES[residual.dtype], residual.shape[-1], strides
+
+
+def int8_conv2d(
+    x: Tensor, weight: Tensor, a_scale: Tensor, w_scale: Tensor, bias: Tensor | None,
+    kh: int, kw: int, sh: int, sw: int, ph: int, pw: int, dh: int, dw: int, *, relu: bool = False,
+    residual: Tensor | None = None, out_scale: Tensor | None = None, gelu: bool = False,
+) -> Tensor:
+    """``x`` int8 ``[B, H, W, Cin]`` (packed), ``weight`` int8 ``[Cout, kh*kw*Cin]`` (ky, kx, c) -> BF16
+    ``[B, Ho, Wo, Cout]``, or int8 with ``out_scale``."""
+    b, h, w, cin = x.shape
+    cout = weight.shape[0]
+    ho, wo = conv_output_size(h, w, kh, kw, sh, sw, ph, pw, dh, dw)
+    x = x.contiguous()
+    weight = weight.contiguous()
+    a_scale = a_scale.to(device=x.device, dtype=torch.float32).reshape(1).contiguous()
+    w_scale = w_scale.to(device=x.device, dtype=torch.float32).contiguous()
+    bias, bias_code = _bias_args(bias, x.device)
+    res, res_code, res_channels, res_strides = _residual_args(residual, x.device, (b, ho, wo, cout))
+    if out_scale is not None:
+        out_scale = out_scale.to(device=x.device, dtype=torch.float32).reshape(1).contiguous()
+    out = torch.empty(b, ho, wo, cout, device=x.device, dtype=torch.int8 if out_scale is not None else torch.bfloat16)
+    _lib.call(
+        "fim_int8_conv2d", x.data_ptr(), b, h, w, cin, weight.data_ptr(), cout, a_scale.data_ptr(),
+        w_scale.data_ptr(), _lib.ptr(bias), bias_code, kh, kw, sh, sw, ph, pw, dh, dw, int(relu), int(gelu),
+        _lib.ptr(res), res_code, res_channels, res_strides, _lib.ptr(out_scale), out.data_ptr(), _lib.stream_of(x),
+        what=f"int8_conv2d {tuple(x.shape)} -> {cout} k{kh}x{kw}",
+    )
+    return out
+
+
+def mxfp8_conv2d(
+    x: Tensor, channel_exponent: Tensor, weight: Tensor, weight_exponent: Tensor, bias: Tensor | None,
+    kh: int, kw: int, sh: int, sw: int, ph: int, pw: int, dh: int, dw: int, *, relu: bool = False,
+    residual: Tensor | None = None, out_exponent: Tensor | None = None, gelu: bool = False,
+) -> Tensor:
+    """``x`` E4M3 ``[B, H, W, Cin]`` (``Cin % 32 == 0``), ``channel_exponent`` int8 ``[Cin / 32]``, ``weight`` E4M3
+    ``[Cout, kh*kw*Cin]`` with ``weight_exponent`` ``[Cout, kh*kw*Cin / 32]`` -> BF16 ``[B, Ho, Wo, Cout]``, or E4M3
+    with ``out_exponent``."""
+    b, h, w, cin = x.shape
+    cout = weight.shape[0]
+    ho, wo = conv_output_size(h, w, kh, kw, sh, sw, ph, pw, dh, dw)
+    x = x.contiguous()
+    weight = weight.contiguous()
+    channel_exponent = channel_exponent.to(device=x.device, dtype=torch.int8).contiguous()
+    weight_exponent = weight_exponent.to(device=x.device, dtype=torch.int8).contiguous()
+    bias, bias_code = _bias_args(bias, x.device)
+    res, res_code, res_channels, res_strides = _residual_args(residual, x.device, (b, ho, wo, cout))
+    if out_exponent is not None:
+        out_exponent = out_exponent.to(device=x.device, dtype=torch.int8).contiguous()
+    out = torch.empty(b, ho, wo, cout, device=x.device,
+                      dtype=torch.float8_e4m3fn if out_exponent is not None else torch.bfloat16)
+    _lib.call(
+        "fim_mxfp8_conv2d", x.data_ptr(), b, h, w, cin, channel_exponent.data_ptr(), weight.data_ptr(), cout,
+        weight_exponent.data_ptr(), _lib.ptr(bias), bias_code, kh, kw, sh, sw, ph, pw, dh, dw, int(relu), int(gelu),
+        _lib.ptr(res), res_code, res_channels, res_strides, _lib.ptr(out_exponent), out.data_ptr(),
+        _lib.stream_of(x), what=f"mxfp8_conv2d {tuple(x.shape)} -> {cout} k{kh}x{kw}",
+    )
+    return out
+
+
+# -- depthwise 5x5 producers ------------------------------------------------------------------------------------
+
+_DW_MX_DYNAMIC, _DW_INT8, _DW_BF16, _DW_MX_STATIC = 0, 1, 2, 3
+
+
+def _nhwc_bf16(value: Tensor) -> Tensor:
+    """``[B, C, H, W]`` -> its channels-last memory as a packed BF16 ``[B, H, W, C]`` (rounded to BF16 on load, as the
+    references do with ``value.to(torch.bfloat16)``)."""
+    if value.dtype != torch.bfloat16:
+        value = value.to(torch.bfloat16)
+    return value.permute(0, 2, 3, 1).contiguous()
+
+
+def _dw_launch(value: Tensor, weight: Tensor, bias: Tensor, act: int, mode: int, scale=None, exponent=None,
+               want_exponent: bool = False, want_swizzled: bool = False):
+    batch, channels, height, width = value.shape
+    x = _nhwc_bf16(value)
+    weight = weight.to(device=value.device, dtype=torch.bfloat16).contiguous()
+    bias = bias.to(device=value.device, dtype=torch.float32).contiguous()
+    rows = batch * height * width
+    out_dtype = {_DW_MX_DYNAMIC: torch.float8_e4m3fn, _DW_INT8: torch.int8, _DW_BF16: torch.bfloat16,
+                 _DW_MX_STATIC: torch.float8_e4m3fn}[mode]
+    out = torch.empty(rows, channels, device=value.device, dtype=out_dtype)
+    exponent_out = torch.empty(rows, channels // 32, device=value.device, dtype=torch.int8) if want_exponent else None
+    swizzled = quant.swizzled_buffer(rows, channels // 32, value.device) if want_swizzled else None
+    if scale is not None:
+        scale = scale.to(device=value.device, dtype=torch.float32).reshape(1).contiguous()
+    if exponent is not None:
+        exponent = exponent.to(device=value.device, dtype=torch.int8).contiguous()
+    _lib.call(
+        "fim_depthwise5x5", x.data_ptr(), batch, height, width, channels, weight.data_ptr(), bias.data_ptr(), act,
+        mode, _lib.ptr(scale), _lib.ptr(exponent), out.data_ptr(), _lib.ptr(exponent_out), _lib.ptr(swizzled),
+        _lib.stream_of(value), what=f"depthwise5x5 {tuple(value.shape)}",
+    )
+    return out, exponent_out, swizzled
+
+
+def depthwise5x5_relu_mxfp8(value: Tensor, weight: Tensor, bias: Tensor) -> tuple[Tensor, Tensor]:
+    """E4M3 ``[B*H*W, C]`` and the swizzled E8M0 scales of ``relu(dwconv5x5(value) + bias)``."""
+    out, _, swizzled = _dw_launch(value, weight, bias, 0, _DW_MX_DYNAMIC, want_swizzled=True)
+    return out, swizzled.view(torch.float8_e8m0fnu)
+
+
+def depthwise5x5_relu_int8(value: Tensor, weight: Tensor, bias: Tensor, scale: Tensor) -> Tensor:
+    """int8 ``[B*H*W, C]``: ``relu(dwconv5x5(value) + bias)`` rounded to BF16, statically quantized."""
+    return _dw_launch(value, weight, bias, 0, _DW_INT8, scale=scale)[0]
+
+
+def depthwise5x5_gelu(value: Tensor, weight: Tensor, bias: Tensor, *, scale: Tensor | None = None,
+                      exponent: Tensor | None = None) -> Tensor:
+    """``gelu(bf16(dwconv5x5(value) + bias))`` rounded to BF16 -> BF16 ``[B*H*W, C]``; with ``scale`` that tensor
+    statically quantized to INT8, with ``exponent`` (``[C/32]``) to E4M3."""
+    if scale is not None and exponent is not None:
+        raise ValueError("scale (INT8) and exponent (MXFP8) are exclusive")
+    mode = _DW_INT8 if scale is not None else _DW_MX_STATIC if exponent is not None else _DW_BF16
+    return _dw_launch(value, weight, bias, 1, mode, scale=scale, exponent=exponent)[0]
+
+
+# -- eligibility ----------------------------------------------------------------------------------------------------
+
+
+def eligible_int8_conv2d(x, weight, a_scale, w_scale, bias, kh, kw, sh, sw, ph, pw, dh, dw, **_) -> bool:
+    return (
+        isinstance(x, Tensor) and is_gfx950(x.device) and x.ndim == 4 and x.dtype == torch.int8
+        and weight.dtype == torch.int8 and tuple(weight.shape) == (weight.shape[0], kh * kw * x.shape[-1])
+        and a_scale.numel() == 1 and w_scale.numel() == weight.shape[0]
+        and (bias is None or bias.numel() == weight.shape[0])
+    )
+
+
+def eligible_mxfp8_conv2d(x, channel_exponent, weight, weight_exponent, bias, kh, kw, sh, sw, ph, pw, dh, dw,
+                          **kwargs) -> bool:
+    out_exponent = kwargs.get("out_exponent")
+    return (
+        isinstance(x, Tensor) and is_gfx950(x.device) and x.ndim == 4 and x.dtype == torch.float8_e4m3fn
+        and x.shape[-1] % 32 == 0 and weight.dtype == torch.float8_e4m3fn
+        and tuple(weight.shape) == (weight.shape[0], kh * kw * x.shape[-1])
+        and tuple(weight_exponent.shape) == (weight.shape[0], kh * kw * x.shape[-1] // 32)
+        and tuple(channel_exponent.shape) == (x.shape[-1] // 32,)
+        and (bias is None or bias.numel() == weight.shape[0])
+        and (out_exponent is None or (weight.shape[0] % 32 == 0 and out_exponent.numel() == weight.shape[0] // 32))
+    )
+
+
+def eligible_depthwise(value: Tensor, weight: Tensor, bias: Tensor, *rest, **kwargs) -> bool:
+    return (
+        isinstance(value, Tensor) and is_gfx950(value.device) and value.ndim == 4 and value.shape[1] % 32 == 0
+        and tuple(weight.shape) == (25, value.shape[1]) and tuple(bias.shape) == (value.shape[1],)
+        and (kwargs.get("exponent") is None or kwargs["exponent"].numel() == value.shape[1] // 32)
+    )

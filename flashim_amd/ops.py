@@ -1,0 +1,45 @@
+"""The ops of the quantized implicit-GEMM conv path, declared with FlashIM's names (``flashim/ops/conv.py``,
+``flashim/ops/quantize.py``) on this package's registry, and this backend's impls registered for the ``"rocm"``
+dispatch key with the gfx950 ISA features. Usage mirrors FlashIM: ``ops.int8_conv2d(...)`` dispatches,
+``ops.int8_conv2d.get("hip")`` pins the HIP impl, ``ops.int8_conv2d.explain(...)`` says why.
+
+The declarations carry no torch implementation (see :mod:`flashim_amd.registry`): a call no HIP impl accepts raises
+instead of computing on another path.
+"""
+
+from __future__ import annotations
+
+from flashim_amd.backends.hip import conv as _conv
+from flashim_amd.backends.hip import quantize as _quantize
+from flashim_amd.platforms import Feature
+from flashim_amd.registry import (  # noqa: F401  (re-exported API)
+    OPS, REFERENCE, BoundOp, DeviceSpec, Op, call_counts, configure, reset_call_counts, set_strict,
+)
+
+# declarations (FlashIM names)
+quantize_mxfp8 = Op("quantize_mxfp8")
+quantize_int8 = Op("quantize_int8")
+int8_conv2d = Op("int8_conv2d", composite=True)
+mxfp8_conv2d = Op("mxfp8_conv2d", composite=True)
+depthwise5x5_relu_mxfp8 = Op("depthwise5x5_relu_mxfp8")
+depthwise5x5_relu_int8 = Op("depthwise5x5_relu_int8")
+# this backend's refiner-block producer (folded BatchNorm + GELU)
+depthwise5x5_gelu = Op("depthwise5x5_gelu")
+
+ROCM = DeviceSpec("rocm")
+HIP = "hip"
+
+IMPLS = (
+    # (op name, impl fn, required features, when)
+    ("quantize_mxfp8", _quantize.quantize_mxfp8, (Feature.HIP, Feature.FP8_E4M3), _quantize.eligible_quantize_mxfp8),
+    ("quantize_int8", _quantize.quantize_int8, (Feature.HIP,), _quantize.eligible_quantize_int8),
+    ("int8_conv2d", _conv.int8_conv2d, (Feature.HIP, Feature.MFMA_I8), _conv.eligible_int8_conv2d),
+    ("mxfp8_conv2d", _conv.mxfp8_conv2d, (Feature.HIP, Feature.MFMA_F8F6F4_SCALED), _conv.eligible_mxfp8_conv2d),
+    ("depthwise5x5_relu_mxfp8", _conv.depthwise5x5_relu_mxfp8, (Feature.HIP, Feature.FP8_E4M3),
+     _conv.eligible_depthwise),
+    ("depthwise5x5_relu_int8", _conv.depthwise5x5_relu_int8, (Feature.HIP,), _conv.eligible_depthwise),
+    ("depthwise5x5_gelu", _conv.depthwise5x5_gelu, (Feature.HIP,), _conv.eligible_depthwise),
+)
+
+for _name, _fn, _requires, _when in IMPLS:
+    OPS[_name].register(HIP, device=ROCM, requires=_requires, priority=2, when=_when)(_fn)

@@ -1,0 +1,120 @@
+/* flashim_amd: C ABI of the MI355X (gfx950) quantized implicit-GEMM convolution path.
+ *
+ * Every entry point enqueues its kernels on `stream` and returns without synchronizing. Pointers are device pointers
+ * (borrowed for the duration of the launch; the library allocates nothing). Sizes are element counts, strides are in
+ * elements. The return value is 0 on success, FIM_ERR_INVALID (98) for a null pointer or inconsistent size,
+ * FIM_ERR_UNSUPPORTED (99) for a shape or alignment this library has no kernel for, or a hipError_t code from the
+ * launch. This mirrors the CUDA C++ backend's launch convention (flashim/backends/cuda/csrc/depthwise.cu:407-412 and
+ * its ctypes caller flashim/backends/cuda/conv.py:135-145): plain pointers, ints and the stream, nonzero = failure.
+ *
+ * Floating activation dtype codes: 0 = float32, 1 = bfloat16, 2 = float16.
+ * Byte formats: int8 (two's complement), E4M3 = OCP float8_e4m3fn, MX exponents = unbiased int8 (2^e), E8M0 = e + 127.
+ */
+#ifndef FLASHIM_AMD_H
+#define FLASHIM_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* hipStream_t;
+
+#define FIM_OK 0
+#define FIM_ERR_INVALID 98
+#define FIM_ERR_UNSUPPORTED 99
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int fim_version(void);
+
+/* ---- quantizers -------------------------------------------------------------------------------------------- */
+
+/* Static per-tensor INT8: out[b,h,w,c] = clamp(round_half_even(x[b,h,w,c] * channel_scale[c] / *scale), +-127).
+ * x is [B, H, W, C] with element strides (sb, sh, sw, sc): the NHWC view of NCHW memory is read in place; out is
+ * packed [B, H, W, C]. channel_scale may be NULL. Replaces the impl of ops.quantize_int8
+ * (flashim/ops/quantize.py:91-100; reference quant/tensor.py:148-151, quant/formats/int8.py:24-27). */
+int fim_quantize_int8(const void* x, int dtype, int64_t B, int64_t H, int64_t W, int64_t C, int64_t sb, int64_t sh,
+                      int64_t sw, int64_t sc, const float* scale, const float* channel_scale, int8_t* out,
+                      hipStream_t stream);
+
+/* Static block-32 MXFP8: out[r, c] = e4m3(clamp(x[r, c] / 2^exponent[c / 32], +-448)) for c < C, 0 for
+ * C <= c < Cpad (Cpad = C rounded up to 32). Same input geometry as fim_quantize_int8; out is [B*H*W, Cpad].
+ * Replaces ops.quantize_mxfp8 (flashim/ops/quantize.py:80-85; reference quant/tensor.py:97-121). */
+int fim_quantize_mxfp8(const void* x, int dtype, int64_t B, int64_t H, int64_t W, int64_t C, int64_t sb, int64_t sh,
+                       int64_t sw, int64_t sc, const int8_t* exponent, uint8_t* out, int64_t Cpad,
+                       hipStream_t stream);
+
+/* Dynamic per-(row, 32) MXFP8 of a [rows, K] matrix (K % 32 == 0, row stride in elements, 16-byte aligned rows):
+ * E4M3 out [rows, K] (packed), exponent [rows, K/32] int8 (may be NULL), and the E8M0 scales in cuBLAS' 128x4
+ * swizzled layout (may be NULL; its padding bytes are not written, the caller zero-fills them).
+ * Replaces quant/formats/mx.py:50-60 (quantize_dynamic_2d) + :67-86 (swizzle_scales); also packs QuantizedWeight
+ * (quant/tensor.py:77-87) from a padded weight. */
+int fim_quantize_mxfp8_dynamic(const void* x, int dtype, int64_t rows, int64_t K, int64_t row_stride, uint8_t* out,
+                               int8_t* exponent, uint8_t* swizzled, hipStream_t stream);
+
+/* Per-row symmetric INT8: scale[r] = safe_scale(amax_r / 127) (reciprocal = 0, IEEE division: weight_scales,
+ * quant/formats/int8.py:19-21) or safe_scale(amax_r * (1/127)) (reciprocal = 1: ops.quantize_int8_rows,
+ * flashim/ops/quantize.py:148-157); out[r, k] = clamp(round_half_even(x[r, k] / scale[r]), +-127). out is packed
+ * [rows, K]. */
+int fim_quantize_int8_rows(const void* x, int dtype, int64_t rows, int64_t K, int64_t row_stride, int reciprocal,
+                           int8_t* out, float* scale, hipStream_t stream);
+
+/* Static exponent calibration: exponent[g] = scale_exponent_from_amax(max over rows and the 32 channels of block g
+ * of |x|), g < ceil(C / 32) (quant/formats/mx.py:41-47). workspace: ceil(C/32) uint32 of caller memory. */
+int fim_calibrate_block32(const void* x, int dtype, int64_t rows, int64_t C, int64_t row_stride, uint32_t* workspace,
+                          int8_t* exponent, hipStream_t stream);
+
+/* ---- implicit-GEMM convolutions ----------------------------------------------------------------------------- */
+
+/* INT8 conv2d, groups == 1: x int8 [B, H, W, Cin] packed; weight int8 [Cout, kh*kw*Cin] in (ky, kx, c) order;
+ * a_scale one float, w_scale [Cout]; bias [Cout] (bias_dtype 0 f32 / 1 bf16) or NULL. Epilogue:
+ * y = float(acc) * (a_scale * w_scale[n]) + bias[n] (two roundings); ReLU (when no residual); BF16; GELU if gelu;
+ * residual [B, Ho, Wo, res_channels] with res_strides[4] added in FP32 (+ReLU) then BF16. out: BF16 [B, Ho, Wo, Cout],
+ * or, when out_scale != NULL, that BF16 result statically quantized to INT8 with *out_scale.
+ * Replaces ops.int8_conv2d (flashim/ops/conv.py:174-206; backend signature flashim/backends/triton/conv.py:816-833).
+ * gelu has no counterpart in int8_conv2d: it is int8_linear's GELU epilogue (flashim/ops/gemm.py:94-95). */
+int fim_int8_conv2d(const int8_t* x, int64_t B, int64_t H, int64_t W, int64_t Cin, const int8_t* weight, int64_t Cout,
+                    const float* a_scale, const float* w_scale, const void* bias, int bias_dtype, int kh, int kw,
+                    int sh, int sw, int ph, int pw, int dh, int dw, int relu, int gelu, const void* residual,
+                    int res_dtype, int64_t res_channels, const int64_t* res_strides, const float* out_scale,
+                    void* out, hipStream_t stream);
+
+/* Static MXFP8 conv2d, groups == 1: x E4M3 [B, H, W, Cin] (Cin % 32 == 0) with channel_exponent [Cin/32] shared by
+ * every tap; weight E4M3 [Cout, kh*kw*Cin] (ky, kx, c) with weight_exponent [Cout, kh*kw*Cin/32]. FP32 accumulation on
+ * block-scaled MFMA; epilogue y = acc + bias, then as fim_int8_conv2d; out BF16 [B, Ho, Wo, Cout], or with
+ * out_exponent [Cout/32] (Cout % 32 == 0) that BF16 result statically quantized to E4M3.
+ * Replaces ops.mxfp8_conv2d (flashim/ops/conv.py:309-342; backend signature flashim/backends/triton/conv.py:1195-1238). */
+int fim_mxfp8_conv2d(const uint8_t* x, int64_t B, int64_t H, int64_t W, int64_t Cin, const int8_t* channel_exponent,
+                     const uint8_t* weight, int64_t Cout, const int8_t* weight_exponent, const void* bias,
+                     int bias_dtype, int kh, int kw, int sh, int sw, int ph, int pw, int dh, int dw, int relu, int gelu,
+                     const void* residual, int res_dtype, int64_t res_channels, const int64_t* res_strides,
+                     const int8_t* out_exponent, void* out, hipStream_t stream);
+
+/* ---- depthwise 5x5 producers -------------------------------------------------------------------------------- */
+
+/* Depthwise 5x5, pad 2: x BF16 NHWC [B, H, W, C] (channels-last [B, C, H, W]), weight BF16 [25, C] (ky, kx major),
+ * bias FP32 [C], C % 32 == 0. act 0: relu(conv + bias) in FP32; act 1: gelu(bf16(conv + bias)) rounded to BF16.
+ * out_mode 0: dynamic per-(pixel, 32) MXFP8, E4M3 out [B*H*W, C] + exponent_out [B*H*W, C/32] and/or the swizzled
+ * E8M0 bytes (either may be NULL); 1: static INT8 of the BF16-rounded value with *scale; 2: BF16 out;
+ * 3: static MXFP8 with exponent [C/32]. act 0 + mode 0 replaces ops.depthwise5x5_relu_mxfp8 (flashim/ops/conv.py:30-44),
+ * act 0 + mode 1 replaces ops.depthwise5x5_relu_int8 (flashim/ops/conv.py:50-61; the CUDA launcher it mirrors is
+ * launch_dw5x5_relu_int8, flashim/backends/cuda/csrc/depthwise.cu:407-412). */
+int fim_depthwise5x5(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t C, const uint16_t* weight,
+                     const float* bias, int act, int out_mode, const float* scale, const int8_t* exponent, void* out,
+                     int8_t* exponent_out, uint8_t* swizzled, hipStream_t stream);
+
+/* ---- test hooks ------------------------------------------------------------------------------------------------ */
+
+/* E4M3 encodings of n floats with the hardware conversion the kernels use (out[i]) and with the software encoder
+ * (out[n + i]); x must be pre-clamped to +-448. Lets the tests check the two agree on the device. */
+int fim_test_e4m3(const float* x, int64_t n, uint8_t* out, hipStream_t stream);
+
+/* MX exponents of n FP32 amax values with the device rule (quant/formats/mx.py:22-26). */
+int fim_test_mx_exponent(const float* amax, int64_t n, int8_t* out, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHIM_AMD_H */

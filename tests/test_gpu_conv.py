@@ -1,0 +1,210 @@
+"""HIP implicit-GEMM convs vs the oracle.
+
+INT8 (FlashIM's contract tests/ops/test_ops_cuda.py:470-501): the BF16 output is bit-identical to the reference, and so
+are the int32 accumulators (checked through a unit-scale, no-bias run whose outputs are the accumulators rounded to
+BF16, and exactly through the INT8 quant-out path with out_scale chosen so each code is one accumulator step).
+MXFP8 (tests/ops/test_ops_cuda.py:608-637): relative L2 <= 1e-3 and max abs <= 1e-2 x output RMS vs the reference
+(same E4M3 operands and scales, FP32 accumulation in another order)."""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from flashim_amd import ops
+from oracle import reference as ref
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+GEOMETRIES = [
+    (64, 64, 3, 3, 1, 1, 1, 1, 1, 1),
+    (48, 40, 3, 3, 1, 1, 1, 1, 1, 1),  # Cin not a multiple of 32
+    (16, 24, 3, 3, 1, 1, 1, 1, 1, 1),  # Cin < 32
+    (64, 64, 1, 1, 1, 1, 0, 0, 1, 1),  # 1x1
+    (32, 32, 3, 3, 2, 2, 1, 1, 1, 1),  # stride 2
+    (32, 32, 3, 3, 1, 1, 2, 2, 2, 2),  # dilation 2
+    (8, 16, 7, 7, 2, 2, 3, 3, 1, 1),  # 7x7 stride 2, Cin < 32
+    (196, 128, 3, 3, 1, 1, 1, 1, 1, 1),  # Cin > 128, ragged chunk
+    (512, 64, 3, 3, 1, 1, 1, 1, 1, 1),  # four 128-channel chunks per tap
+    (96, 64, 5, 5, 1, 1, 2, 2, 1, 1),  # 5x5
+    (6, 200, 3, 3, 1, 1, 1, 1, 1, 1),  # Cin % 4 != 0 (byte loads), Cout > 128
+]
+
+
+def _int8_inputs(cin, cout, kh, kw, has_bias, shape=(2, 17, 19)):
+    torch.manual_seed(0)
+    x = torch.randint(-127, 127, (*shape, cin), dtype=torch.int8)
+    weight = torch.randint(-127, 127, (cout, kh * kw * cin), dtype=torch.int8)
+    a_scale = torch.tensor(0.017)
+    w_scale = torch.rand(cout) * 0.01 + 0.001
+    bias = torch.randn(cout).to(torch.bfloat16) if has_bias else None
+    return x, weight, a_scale, w_scale, bias
+
+
+def _dev(*ts):
+    return [t.to(DEV) if isinstance(t, torch.Tensor) else t for t in ts]
+
+
+@pytest.mark.parametrize("cin,cout,kh,kw,sh,sw,ph,pw,dh,dw", GEOMETRIES)
+@pytest.mark.parametrize("has_bias", [True, False])
+def test_int8_conv2d_bit_exact(cin, cout, kh, kw, sh, sw, ph, pw, dh, dw, has_bias):
+    x, weight, a_scale, w_scale, bias = _int8_inputs(cin, cout, kh, kw, has_bias)
+    geo = (kh, kw, sh, sw, ph, pw, dh, dw)
+    fast = ops.int8_conv2d.get("hip")(*_dev(x, weight, a_scale, w_scale, bias), *geo).cpu()
+    want = ref.int8_conv2d(x, weight, a_scale, w_scale, bias, *geo)
+    assert fast.shape == want.shape and fast.dtype == torch.bfloat16
+    assert torch.equal(fast, want)
+    fused = ops.int8_conv2d.get("hip")(*_dev(x, weight, a_scale, w_scale, bias), *geo, relu=True).cpu()
+    assert torch.equal(fused, F.relu(fast))
+
+
+@pytest.mark.parametrize("cin,cout,kh,kw,sh,sw,ph,pw,dh,dw", GEOMETRIES[:6])
+def test_int8_conv2d_accumulators_exact(cin, cout, kh, kw, sh, sw, ph, pw, dh, dw):
+    """Unit scales and no bias make the INT8 quant-out code equal to the accumulator wherever |acc| <= 127: the
+    device's int32 accumulators equal the oracle's int64 ones there; the oracle's equal F.conv2d in float64 everywhere."""
+    torch.manual_seed(1)
+    x = torch.randint(-8, 8, (2, 17, 19, cin), dtype=torch.int8)
+    weight = torch.randint(-8, 8, (cout, kh * kw * cin), dtype=torch.int8)
+    one, ones = torch.tensor(1.0), torch.ones(cout)
+    geo = (kh, kw, sh, sw, ph, pw, dh, dw)
+    acc = ref.int8_conv2d_accumulators(x, weight, *geo)
+    got = ops.int8_conv2d.get("hip")(*_dev(x, weight, one, ones, None), *geo, out_scale=torch.tensor(1.0, device=DEV))
+    small = acc.abs() <= 127
+    want = ref.int8_conv2d(x, weight, one, ones, None, *geo, out_scale=torch.tensor(1.0))
+    assert torch.equal(got.cpu(), want)
+    assert torch.equal(got.cpu().long()[small], acc[small])
+    # and the full-range accumulators through F.conv2d in float64 (exact for |acc| < 2^53)
+    exact = F.conv2d(
+        x.permute(0, 3, 1, 2).double(), weight.reshape(cout, kh, kw, cin).permute(0, 3, 1, 2).double(),
+        stride=(sh, sw), padding=(ph, pw), dilation=(dh, dw),
+    ).permute(0, 2, 3, 1).long()
+    assert torch.equal(acc, exact)
+
+
+def test_int8_conv2d_config1():
+    """Config 1: N=1, 128x128, 64 -> 64, 3x3 pad 1; per-tensor activation scale, per-channel weights, fp32 bias."""
+    torch.manual_seed(0)
+    act = torch.randn(1, 64, 128, 128)
+    a_scale = act.abs().amax() / 127
+    x = ref.quantize_int8(act.permute(0, 2, 3, 1), a_scale)
+    w = torch.randn(64, 64, 3, 3) * 0.05
+    wm = w.permute(0, 2, 3, 1).reshape(64, -1)
+    w_scale = ref.weight_scales(wm)
+    wq = ref.quantize_symmetric(wm, w_scale[:, None])
+    bias = torch.randn(64)
+    geo = (3, 3, 1, 1, 1, 1, 1, 1)
+    got = ops.int8_conv2d.get("hip")(*_dev(x, wq, a_scale, w_scale, bias), *geo).cpu()
+    assert torch.equal(got, ref.int8_conv2d(x, wq, a_scale, w_scale, bias, *geo))
+
+
+@pytest.mark.parametrize("relu", [False, True])
+@pytest.mark.parametrize("gelu", [False, True])
+def test_int8_conv2d_epilogues(relu, gelu):
+    x, weight, a_scale, w_scale, bias = _int8_inputs(64, 96, 3, 3, True)
+    geo = (3, 3, 1, 1, 1, 1, 1, 1)
+    residual = torch.randn(2, 17, 19, 80).to(torch.bfloat16)  # fewer channels than Cout
+    out_scale = torch.tensor(0.05)
+    for kwargs in ({}, {"residual": residual}, {"out_scale": out_scale}, {"residual": residual, "out_scale": out_scale}):
+        got = ops.int8_conv2d.get("hip")(*_dev(x, weight, a_scale, w_scale, bias), *geo, relu=relu, gelu=gelu,
+                                          **{k: v.to(DEV) for k, v in kwargs.items()}).cpu()
+        want = ref.int8_conv2d(x, weight, a_scale, w_scale, bias, *geo, relu=relu, gelu=gelu, **kwargs)
+        if gelu:
+            # GELU's erf: the device math library and torch's CPU erf differ by about an ulp, which 1 + erf(x) turns
+            # into a large relative error where GELU's output is tiny (x < -3): compare with an absolute floor
+            diff = (got.float() - want.float()).abs()
+            if got.dtype == torch.int8:
+                assert diff.max() <= 1 and (got != want).float().mean() < 1e-3
+            else:
+                assert (diff <= want.float().abs() * 2**-7 + 2**-12).all()
+        else:
+            assert torch.equal(got, want), kwargs.keys()
+
+
+def _mx_inputs(cin, cout, kh, kw, has_bias, seed=0):
+    torch.manual_seed(seed)
+    x = (torch.randn(2, 17, 19, cin) * 3).to(torch.float8_e4m3fn)
+    channel_exponent = torch.randint(-6, 3, (cin // 32,), dtype=torch.int8)
+    weight = (torch.randn(cout, kh * kw * cin) * 2).to(torch.float8_e4m3fn)
+    weight_exponent = torch.randint(-9, -3, (cout, kh * kw * cin // 32), dtype=torch.int8)
+    bias = torch.randn(cout).to(torch.bfloat16) if has_bias else None
+    return x, channel_exponent, weight, weight_exponent, bias
+
+
+def _assert_mx_close(fast, want):
+    """Relative L2 <= 1e-3; per element |diff| <= max(1e-2 x output RMS, 2^-7 |want|). The second term is one BF16
+    rounding step of the reference value: two FP32 accumulation orders flip the final BF16 rounding of some outputs,
+    and at |y| > 2.56 x RMS that single flip alone exceeds 1e-2 x RMS."""
+    fast, want = fast.float(), want.float()
+    rms = want.pow(2).mean().sqrt()
+    rel = (fast - want).norm() / want.norm()
+    assert rel <= 1e-3, rel
+    assert ((fast - want).abs() <= torch.maximum(1e-2 * rms, want.abs() * 2**-7)).all()
+
+
+MX_GEOMETRIES = [
+    (64, 64, 3, 3, 1, 1, 1, 1, 1, 1),
+    (224, 128, 3, 3, 1, 1, 1, 1, 1, 1),
+    (512, 64, 3, 3, 1, 1, 1, 1, 1, 1),
+    (96, 64, 5, 5, 1, 1, 2, 2, 1, 1),
+    (64, 196, 3, 3, 2, 2, 1, 1, 1, 1),
+    (32, 32, 3, 3, 1, 1, 2, 2, 2, 2),
+    (128, 128, 1, 1, 1, 1, 0, 0, 1, 1),
+]
+
+
+@pytest.mark.parametrize("cin,cout,kh,kw,sh,sw,ph,pw,dh,dw", MX_GEOMETRIES)
+@pytest.mark.parametrize("has_bias", [True, False])
+def test_mxfp8_conv2d(cin, cout, kh, kw, sh, sw, ph, pw, dh, dw, has_bias):
+    args = _mx_inputs(cin, cout, kh, kw, has_bias)
+    geo = (kh, kw, sh, sw, ph, pw, dh, dw)
+    fast = ops.mxfp8_conv2d.get("hip")(*_dev(*args), *geo).cpu()
+    want = ref.mxfp8_conv2d(*args, *geo)
+    assert fast.shape == want.shape and fast.dtype == torch.bfloat16
+    _assert_mx_close(fast, want)
+    fused = ops.mxfp8_conv2d.get("hip")(*_dev(*args), *geo, relu=True).cpu()
+    assert torch.equal(fused, F.relu(fast))
+
+
+def test_mxfp8_conv2d_matches_float64_conv():
+    """Independent of the oracle: dequantized operands through F.conv2d in float64."""
+    x, ce, w, we, bias = _mx_inputs(64, 96, 3, 3, True, seed=7)
+    geo = (3, 3, 1, 1, 1, 1, 1, 1)
+    fast = ops.mxfp8_conv2d.get("hip")(*_dev(x, ce, w, we, bias), *geo).cpu().double()
+    xd = x.double() * torch.exp2(ce.double()).repeat_interleave(32)
+    wd = (w.double() * torch.exp2(we.double()).repeat_interleave(32, dim=1)).reshape(96, 3, 3, 64).permute(0, 3, 1, 2)
+    exact = F.conv2d(xd.permute(0, 3, 1, 2), wd, bias.double(), padding=1).permute(0, 2, 3, 1)
+    magnitude = F.conv2d(xd.abs().permute(0, 3, 1, 2), wd.abs(), bias.double().abs(), padding=1).permute(0, 2, 3, 1)
+    # one BF16 rounding of the exact value plus FP32 accumulation error (K = 576 terms)
+    assert ((fast - exact).abs() <= exact.abs() * 2**-8 + magnitude * 2**-14).all()
+
+
+@pytest.mark.parametrize("relu", [False, True])
+@pytest.mark.parametrize("gelu", [False, True])
+def test_mxfp8_conv2d_epilogues(relu, gelu):
+    x, ce, w, we, bias = _mx_inputs(64, 96, 3, 3, True, seed=3)
+    geo = (3, 3, 1, 1, 1, 1, 1, 1)
+    residual = torch.randn(2, 17, 19, 80).to(torch.bfloat16)
+    out_exponent = torch.tensor([-4, -3, -2], dtype=torch.int8)
+    for kwargs in ({}, {"residual": residual}):
+        got = ops.mxfp8_conv2d.get("hip")(*_dev(x, ce, w, we, bias), *geo, relu=relu, gelu=gelu,
+                                           **{k: v.to(DEV) for k, v in kwargs.items()}).cpu()
+        want = ref.mxfp8_conv2d(x, ce, w, we, bias, *geo, relu=relu, gelu=gelu, **kwargs)
+        _assert_mx_close(got, want)
+    # quant-out: the E4M3 codes of the BF16 result quantized with out_exponent (chained = separate quantize)
+    got_bf16 = ops.mxfp8_conv2d.get("hip")(*_dev(x, ce, w, we, bias), *geo, relu=relu, gelu=gelu).cpu()
+    got_q = ops.mxfp8_conv2d.get("hip")(*_dev(x, ce, w, we, bias), *geo, relu=relu, gelu=gelu,
+                                         out_exponent=out_exponent.to(DEV)).cpu()
+    assert torch.equal(got_q.view(torch.uint8), ref.quantize_static(got_bf16, out_exponent).view(torch.uint8))
+
+
+def test_repeated_launches_identical():
+    """Race guard (tests/ops/test_ops_cuda.py:81-97 style): repeated launches give the same bytes."""
+    args = _dev(*_mx_inputs(128, 128, 3, 3, True))
+    geo = (3, 3, 1, 1, 1, 1, 1, 1)
+    first = ops.mxfp8_conv2d.get("hip")(*args, *geo)
+    for _ in range(10):
+        assert torch.equal(ops.mxfp8_conv2d.get("hip")(*args, *geo), first)
+    iargs = _dev(*_int8_inputs(96, 200, 3, 3, True))
+    ifirst = ops.int8_conv2d.get("hip")(*iargs, *geo)
+    for _ in range(10):
+        assert torch.equal(ops.int8_conv2d.get("hip")(*iargs, *geo), ifirst)

@@ -1,0 +1,49 @@
+"""Device numerics: the hardware E4M3 conversion the kernels use agrees byte for byte with the software encoder and
+with torch (every BF16 value and random FP32 values, subnormals and signed zeros included), and the device MX
+exponent rule agrees with the oracle's ceil(log2(amax / 448)) at every power-of-two boundary."""
+
+import pytest
+import torch
+
+from flashim_amd import _lib
+from oracle import reference as ref
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _device_e4m3(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    x = x.to(DEV).float().contiguous()
+    out = torch.empty(2 * x.numel(), device=DEV, dtype=torch.uint8)
+    _lib.call("fim_test_e4m3", x.data_ptr(), x.numel(), out.data_ptr(), _lib.stream_of(x))
+    out = out.cpu()
+    return out[: x.numel()], out[x.numel():]
+
+
+def test_e4m3_hardware_matches_software_and_torch():
+    bf16 = torch.arange(0, 65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).float()
+    bf16 = bf16[torch.isfinite(bf16)].clamp(-448, 448)
+    torch.manual_seed(0)
+    rnd = (torch.randn(1 << 21) * torch.exp2(torch.randint(-24, 10, (1 << 21,)).float())).clamp(-448, 448)
+    ties = torch.tensor([2.0**-10, -(2.0**-10), 3 * 2.0**-10, 0.0, -0.0, 448.0, -448.0, 1.0625, 1.1875, 2.0**-6])
+    for x in (bf16, rnd, ties):
+        hw, sw = _device_e4m3(x)
+        want = x.to(torch.float8_e4m3fn).view(torch.uint8)
+        assert torch.equal(sw, want)
+        assert torch.equal(hw, want), f"{(hw != want).sum().item()} hardware E4M3 mismatches"
+
+
+def test_mx_exponent_matches_oracle():
+    torch.manual_seed(0)
+    ks = torch.arange(-149, 128).double()
+    bnd = (torch.exp2(ks)[:, None] * (1 + torch.arange(0, 64).double()[None] * 2.0**-23) * 448).float().flatten()
+    amax = torch.cat([
+        torch.tensor([0.0, 448.0, 449.0, 1.0, 1e-30, 1e-45, 3e38]),
+        torch.rand(1 << 20) * torch.exp2(torch.randint(-140, 120, (1 << 20,)).float()),
+        bnd, bnd.nextafter(torch.tensor(0.0)), bnd.nextafter(torch.tensor(3e38)),
+    ])
+    amax = amax[torch.isfinite(amax)].contiguous()
+    out = torch.empty(amax.numel(), device=DEV, dtype=torch.int8)
+    a = amax.to(DEV)
+    _lib.call("fim_test_mx_exponent", a.data_ptr(), a.numel(), out.data_ptr(), _lib.stream_of(a))
+    assert torch.equal(out.cpu(), ref.scale_exponent_from_amax(amax))
