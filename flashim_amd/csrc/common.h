@@ -23,6 +23,23 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed BF16 (low = a), round to nearest even: one v_cvt_pk_bf16_f32 on gfx950. The GPU tests check it
+// against the software rounding of numerics.h (f32_to_bf16) and torch over every BF16 neighbourhood class.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  v2f v = {a, b};
+  v2bf p = __builtin_convertvector(v, v2bf);
+  return __builtin_bit_cast(uint32_t, p);
+}
+
+// a and b rounded to BF16 and widened back (torch's `.to(torch.bfloat16).float()` on each).
+__device__ __forceinline__ void round_bf16x2(float& a, float& b) {
+  const uint32_t p = pack_bf16x2(a, b);
+  a = u2f(p << 16);
+  b = u2f(p & 0xffff0000u);
+}
 
 template <int DT>
 __device__ __forceinline__ float load_elem(const void* p, int64_t i);
@@ -60,6 +77,33 @@ __device__ __forceinline__ uint8_t e4m3(float a) {
   return (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(a, a, 0, false) & 0xff);
 #endif
 }
+
+// GELU, erf form: 0.5 x erfc(-x / sqrt 2), with erfc from the Chebyshev fit of Numerical Recipes ("erfcc",
+// fractional error < 1.2e-7 everywhere): branch-free, ~20 VALU ops. Evaluating erfc directly also keeps the negative
+// tail accurate, where torch's 0.5 x (1 + erf(x / sqrt 2)) cancels (there the two differ by far less than a BF16 ulp of
+// the layer's values, though not of the tiny tail values themselves).
+__device__ __forceinline__ float gelu_erf(float x) {
+  const float z = x * -0.70710678118654752440f;
+  const float az = fabsf(z);
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, az, 1.0f));
+  float p = fmaf(t, 0.17087277f, -0.82215223f);
+  p = fmaf(t, p, 1.48851587f);
+  p = fmaf(t, p, -1.13520398f);
+  p = fmaf(t, p, 0.27886807f);
+  p = fmaf(t, p, -0.18628806f);
+  p = fmaf(t, p, 0.09678418f);
+  p = fmaf(t, p, 0.37409196f);
+  p = fmaf(t, p, 1.00002368f);
+  p = fmaf(t, p, -1.26551223f);
+  const float e = t * __expf(fmaf(-az, az, p));  // erfc(|z|)
+  const float erfc_z = z >= 0.0f ? e : 2.0f - e;
+  return 0.5f * x * erfc_z;
+}
+
+// Workgroup barrier for LDS hand-offs that leaves global loads in flight: waits only for this wave's LDS operations
+// (lgkmcnt), unlike __syncthreads(), whose workgroup-scope fence also drains every outstanding global load (vmcnt) and
+// so serializes prefetches with the MFMAs. The "memory" clobber keeps the compiler from moving memory accesses across.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 inline int launch_status() {
   hipError_t err = hipGetLastError();

@@ -24,7 +24,6 @@ enum { DW_MX_DYNAMIC = 0, DW_INT8 = 1, DW_BF16 = 2, DW_MX_STATIC = 3 };
 
 constexpr int DW_TH = 16;
 
-__device__ __forceinline__ float dw_gelu(float x) { return x * 0.5f * (1.0f + erff(x * 0.70710678118654752440f)); }
 
 __device__ __forceinline__ void load4_bf16(const uint16_t* p, float* v) {
   uint2 q = *reinterpret_cast<const uint2*>(p);
@@ -67,7 +66,11 @@ __global__ __launch_bounds__(256) void dw5x5_kernel(const DwArgs a) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) bias[i] = a.bias[c + i];
   float oscale = 0.f, oinv = 1.f;
-  if (OUT == DW_INT8) oscale = *a.scale;
+  float oinv8 = 1.f;
+  if (OUT == DW_INT8) {
+    oscale = *a.scale;
+    oinv8 = __fdiv_rn(1.0f, oscale);
+  }
   if (OUT == DW_MX_STATIC) oinv = exp2_int(-(int)a.expo[c >> 5]);
 
   float acc[5][4];
@@ -112,7 +115,7 @@ __global__ __launch_bounds__(256) void dw5x5_kernel(const DwArgs a) {
         if (ACT == ACT_RELU) {
           y[i] = fmaxf(t, 0.f);
         } else {
-          y[i] = round_bf16(dw_gelu(round_bf16(t)));
+          y[i] = round_bf16(gelu_erf(round_bf16(t)));
         }
       }
       const int64_t row = ((int64_t)b * a.H + oy) * a.W + x;
@@ -143,7 +146,7 @@ __global__ __launch_bounds__(256) void dw5x5_kernel(const DwArgs a) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             float t = ACT == ACT_RELU ? round_bf16(y[i]) : y[i];
-            q |= (uint32_t)(uint8_t)quantize_int8_value(t, oscale) << (8 * i);
+            q |= (uint32_t)(uint8_t)quantize_int8_fast(t, oscale, oinv8) << (8 * i);
           }
           *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.out) + row * a.C + c) = q;
         } else if (OUT == DW_MX_STATIC) {

@@ -10,6 +10,13 @@ __global__ void test_e4m3_kernel(const float* x, int64_t n, uint8_t* out) {
   out[n + i] = f32_to_e4m3_sw(x[i]);
 }
 
+__global__ void test_bf16_kernel(const float* x, int64_t n, uint16_t* out) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[i] = (uint16_t)(pack_bf16x2(x[i], 0.0f) & 0xffffu);
+  out[n + i] = f32_to_bf16(x[i]);
+}
+
 __global__ void test_mx_exponent_kernel(const float* amax, int64_t n, int8_t* out) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) out[i] = (int8_t)mx_exponent_from_amax(amax[i]);
@@ -27,6 +34,13 @@ int fim_test_e4m3(const float* x, int64_t n, uint8_t* out, hipStream_t stream) {
   if (x == nullptr || out == nullptr || n < 0) return FIM_ERR_INVALID;
   if (n == 0) return FIM_OK;
   test_e4m3_kernel<<<dim3((unsigned)cdiv(n, 256)), dim3(256), 0, stream>>>(x, n, out);
+  return launch_status();
+}
+
+int fim_test_bf16(const float* x, int64_t n, uint16_t* out, hipStream_t stream) {
+  if (x == nullptr || out == nullptr || n < 0) return FIM_ERR_INVALID;
+  if (n == 0) return FIM_OK;
+  test_bf16_kernel<<<dim3((unsigned)cdiv(n, 256)), dim3(256), 0, stream>>>(x, n, out);
   return launch_status();
 }
 

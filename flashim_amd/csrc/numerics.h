@@ -162,6 +162,21 @@ FIM_HD int8_t quantize_int8_value(float x, float scale) {
   return (int8_t)(int)q;
 }
 
+#ifdef __HIPCC__
+// quantize_int8_value with the division replaced by a multiply by inv = 1 / scale (correctly rounded), falling back
+// to the IEEE division only where it can matter: x * inv is within a few ulps of the exact quotient, so both round to
+// the same integer unless the quotient sits within 2^-15 of a half-integer (|q| < 128; beyond, both saturate).
+__device__ __forceinline__ int8_t quantize_int8_fast(float x, float scale, float inv) {
+  float y = x * inv;
+  const float fr = y - __builtin_floorf(y);
+  if (fabsf(fr - 0.5f) <= 0x1p-15f) y = __fdiv_rn(x, scale);
+  float q = __builtin_rintf(y);
+  q = q > 127.0f ? 127.0f : q;
+  q = q < -127.0f ? -127.0f : q;
+  return (int8_t)(int)q;
+}
+#endif
+
 // One element of quantize_blocks + .to(float8_e4m3fn): clamp(x / 2^e, +-448) -> E4M3. Division by an exact power of
 // two equals multiplication by its exact reciprocal (one rounding of the same real), so multiply.
 FIM_HD float mx_scale_clamp(float x, float inv_scale) {

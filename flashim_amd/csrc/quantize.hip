@@ -28,13 +28,14 @@ enum { MODE_INT8 = 0, MODE_MX = 1 };
 template <int MODE>
 struct Quantizer {
   float scale;            // INT8 scale
+  float inv;              // INT8 1 / scale
   const float* cs;        // INT8 optional per-channel pre-multiplier (SmoothQuant's 1/s)
   const int8_t* expo;     // MX static exponents [Cpad / 32]
 
   __device__ __forceinline__ uint8_t operator()(float v, int64_t c) const {
     if (MODE == MODE_INT8) {
       if (cs != nullptr) v = v * cs[c];
-      return (uint8_t)quantize_int8_value(v, scale);
+      return (uint8_t)quantize_int8_fast(v, scale, inv);
     } else {
       float inv = exp2_int(-(int)expo[c >> 5]);
       return e4m3(mx_scale_clamp(v, inv));
@@ -69,7 +70,10 @@ template <int DT, int MODE>
 __global__ __launch_bounds__(256) void quantize_rows_vec8(const void* __restrict__ x, Geometry4 g, int packed,
                                                           Quantizer<MODE> qz, const float* __restrict__ scale_ptr,
                                                           uint8_t* __restrict__ out, int64_t Cout) {
-  if (MODE == MODE_INT8) qz.scale = *scale_ptr;
+  if (MODE == MODE_INT8) {
+    qz.scale = *scale_ptr;
+    qz.inv = __fdiv_rn(1.0f, qz.scale);
+  }
   const int64_t groups = Cout >> 3;
   const int64_t total = g.B * g.H * g.W * groups;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
@@ -103,7 +107,10 @@ __global__ __launch_bounds__(256) void quantize_rows_transpose(const void* __res
                                                                Quantizer<MODE> qz, const float* __restrict__ scale_ptr,
                                                                uint8_t* __restrict__ out, int64_t Cout) {
   __shared__ float tile[64][65];
-  if (MODE == MODE_INT8) qz.scale = *scale_ptr;
+  if (MODE == MODE_INT8) {
+    qz.scale = *scale_ptr;
+    qz.inv = __fdiv_rn(1.0f, qz.scale);
+  }
   const int64_t w0 = (int64_t)blockIdx.x * 64;
   const int64_t c0 = (int64_t)blockIdx.y * 64;
   const int64_t bh = blockIdx.z;
@@ -156,7 +163,10 @@ template <int DT, int MODE>
 __global__ __launch_bounds__(256) void quantize_rows_scalar(const void* __restrict__ x, Geometry4 g,
                                                             Quantizer<MODE> qz, const float* __restrict__ scale_ptr,
                                                             uint8_t* __restrict__ out, int64_t Cout) {
-  if (MODE == MODE_INT8) qz.scale = *scale_ptr;
+  if (MODE == MODE_INT8) {
+    qz.scale = *scale_ptr;
+    qz.inv = __fdiv_rn(1.0f, qz.scale);
+  }
   const int64_t total = g.B * g.H * g.W * Cout;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
     int64_t r = i / Cout, c = i - r * Cout;
@@ -287,7 +297,8 @@ __global__ __launch_bounds__(256) void quantize_int8_rows_kernel(const void* __r
   const float eps = 1.1920928955078125e-07f;
   if (!(s > eps) || !__builtin_isfinite(s)) s = eps;
   if (threadIdx.x == 0) scale_out[r] = s;
-  for (int64_t c = threadIdx.x; c < K; c += 256) out[r * K + c] = quantize_int8_value(load_elem<DT>(x, base + c), s);
+  const float inv = __fdiv_rn(1.0f, s);
+  for (int64_t c = threadIdx.x; c < K; c += 256) out[r * K + c] = quantize_int8_fast(load_elem<DT>(x, base + c), s, inv);
 }
 
 // ----- static exponent calibration (amax over rows per 32-channel block) -------------------------------------
@@ -331,7 +342,7 @@ int fim_quantize_int8(const void* x, int dtype, int64_t B, int64_t H, int64_t W,
                       hipStream_t stream) {
   if (x == nullptr || scale == nullptr || out == nullptr || B < 0 || H < 0 || W < 0 || C < 0) return FIM_ERR_INVALID;
   Geometry4 g{B, H, W, C, sb, sh, sw, sc};
-  Quantizer<MODE_INT8> qz{0.0f, channel_scale, nullptr};
+  Quantizer<MODE_INT8> qz{0.0f, 1.0f, channel_scale, nullptr};
   return dispatch_quantize<MODE_INT8>(x, dtype, g, qz, scale, reinterpret_cast<uint8_t*>(out), C, stream);
 }
 
@@ -341,7 +352,7 @@ int fim_quantize_mxfp8(const void* x, int dtype, int64_t B, int64_t H, int64_t W
   if (x == nullptr || exponent == nullptr || out == nullptr || B < 0 || H < 0 || W < 0 || C < 0) return FIM_ERR_INVALID;
   if (Cpad % 32 != 0 || Cpad < C || Cpad - C >= 32) return FIM_ERR_INVALID;
   Geometry4 g{B, H, W, C, sb, sh, sw, sc};
-  Quantizer<MODE_MX> qz{0.0f, nullptr, exponent};
+  Quantizer<MODE_MX> qz{0.0f, 1.0f, nullptr, exponent};
   return dispatch_quantize<MODE_MX>(x, dtype, g, qz, nullptr, out, Cpad, stream);
 }
 

@@ -110,6 +110,10 @@ int fim_depthwise5x5(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t
  * (out[n + i]); x must be pre-clamped to +-448. Lets the tests check the two agree on the device. */
 int fim_test_e4m3(const float* x, int64_t n, uint8_t* out, hipStream_t stream);
 
+/* BF16 roundings of n floats with the hardware conversion the kernels use (out[i]) and with the software rule
+ * (out[n + i]). */
+int fim_test_bf16(const float* x, int64_t n, uint16_t* out, hipStream_t stream);
+
 /* MX exponents of n FP32 amax values with the device rule (quant/formats/mx.py:22-26). */
 int fim_test_mx_exponent(const float* amax, int64_t n, int8_t* out, hipStream_t stream);
 

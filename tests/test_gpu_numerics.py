@@ -47,3 +47,24 @@ def test_mx_exponent_matches_oracle():
     a = amax.to(DEV)
     _lib.call("fim_test_mx_exponent", a.data_ptr(), a.numel(), out.data_ptr(), _lib.stream_of(a))
     assert torch.equal(out.cpu(), ref.scale_exponent_from_amax(amax))
+
+
+def test_bf16_hardware_rounding_matches_torch():
+    """v_cvt_pk_bf16_f32 (the epilogues' rounding) vs the software rule and torch: every BF16 value and its midpoints
+    to the neighbours (the tie cases), their one-ulp perturbations, FP32 subnormals and random values."""
+    base = torch.arange(0, 65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).float()
+    base = base[torch.isfinite(base)]
+    bits = base.view(torch.int32)
+    mids = (bits + 0x8000).view(torch.float32)
+    cases = [base, mids, (bits + 0x7FFF).view(torch.float32), (bits + 0x8001).view(torch.float32),
+             torch.randint(1, 1 << 23, (1 << 16,), dtype=torch.int32).view(torch.float32),
+             torch.randn(1 << 20) * torch.exp2(torch.randint(-140, 120, (1 << 20,)).float())]
+    for x in cases:
+        x = x[torch.isfinite(x)].contiguous()
+        xd = x.to(DEV)
+        out = torch.empty(2 * x.numel(), device=DEV, dtype=torch.int16)
+        _lib.call("fim_test_bf16", xd.data_ptr(), x.numel(), out.data_ptr(), _lib.stream_of(xd))
+        out = out.cpu()
+        want = x.to(torch.bfloat16).view(torch.int16)
+        assert torch.equal(out[x.numel():], want)
+        assert torch.equal(out[: x.numel()], want), f"{(out[: x.numel()] != want).sum().item()} hardware BF16 mismatches"
