@@ -29,6 +29,10 @@ METRIC = "TOPS + % MFMA peak, MXFP8/INT8 implicit-GEMM conv; ms per refiner stac
 PEAK_MX_TFLOPS = 5000.0  # dense MXFP8 / FP8 MFMA, MI355X
 PEAK_INT8_TOPS = 5000.0  # dense INT8 MFMA
 PEAK_HBM_GBS = 8000.0
+# HBM bytes per launch of the config-2 conv from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs (KiB per dispatch), each
+# scaled by what the counter reads for a plain 64 MiB device copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); the runs and the
+# arithmetic are in profiles/conv_mxfp8_1x1_gelu_cfg2.md. Re-measured by hand when the kernel changes.
+CFG2_TRAFFIC_BYTES = int((6557.2 * 2.0 + 22617.2 * 1.0) * 1024)
 DEV = "cuda"
 
 
@@ -37,7 +41,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--only", default=None, help="run one workload only (cfg1|cfg2|cfg3|cfg3q|cfg4|cfg5int8|cfg5mxfp8|copy)"
+    p.add_argument("--only", default=None, help="run one workload only (cfg1|cfg2|cfg3|cfg3q|dw|cfg4|cfg5int8|cfg5mxfp8|copy)"
                                                   " and print its line (profiling runs)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-stack", action="store_true", help="skip configs 4 and 5")
@@ -47,8 +51,10 @@ def parse() -> argparse.Namespace:
 # -- timing ----------------------------------------------------------------------------------------------------
 
 
-def time_graph(fn, steps: int, warmup: int, launches: int = 1) -> float:
-    """Mean ms per replay of ``fn`` captured as a HIP graph (``launches`` kernels per replay)."""
+def time_graph(fn, steps: int, warmup: int, per_graph: int = 10) -> float:
+    """Mean ms per call of ``fn``: ``per_graph`` back-to-back calls are captured in one HIP graph (so the time is the
+    kernels', not the per-replay launch gap), the graph is replayed ``ceil(steps / per_graph)`` times between two HIP
+    events on the stream the kernels run on, and the event time is divided by the calls."""
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
@@ -58,17 +64,19 @@ def time_graph(fn, steps: int, warmup: int, launches: int = 1) -> float:
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        fn()
-    for _ in range(warmup):
+        for _ in range(per_graph):
+            fn()
+    replays = max(1, -(-steps // per_graph))
+    for _ in range(max(1, -(-warmup // per_graph))):
         graph.replay()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
-    for _ in range(steps):
+    for _ in range(replays):
         graph.replay()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    return start.elapsed_time(end) / (replays * per_graph)
 
 
 def time_cpu(fn, budget_s: float = 10.0, max_calls: int = 50, warmup: int = 2) -> tuple[float, int]:
@@ -158,6 +166,20 @@ def cfg3():
         (quantize, {"bytes": q_bytes}, (x_bf16, exponent))
 
 
+def cfg4_depthwise():
+    """The config-4 depthwise producer alone: 5x5 dwconv (folded BN) + GELU -> static MXFP8, NHWC 2x400x400x64."""
+    from flashim_amd import ops
+
+    g = torch.Generator(device="cpu").manual_seed(6)
+    x = torch.randn(2, 400, 400, 64, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(25, 64, generator=g) * 0.2).to(torch.bfloat16).to(DEV)
+    b = (torch.randn(64, generator=g) * 0.1).to(DEV)
+    e = torch.full((2,), -6, dtype=torch.int8, device=DEV)
+    fn = lambda: ops.depthwise5x5_gelu(x.permute(0, 3, 1, 2), w, b, exponent=e)  # noqa: E731
+    pixels = 2 * 400 * 400
+    return fn, {"bytes": pixels * 64 * 2 + pixels * 64}
+
+
 def copy_calibration():
     """A plain device copy of a known size (the PMC traffic calibration)."""
     src = torch.empty(64 << 20, device=DEV, dtype=torch.uint8).fill_(1)
@@ -243,13 +265,16 @@ def main() -> int:
             gemm_line("cfg3_mxfp8_3x3_bn_relu", conv, cinfo)
         if only in (None, "cfg3q"):
             hbm_line("cfg3q_quantize_mxfp8", qfn, qinfo)
+    if only in (None, "dw"):
+        fn, info = cfg4_depthwise()
+        hbm_line("cfg4_depthwise_gelu_mxfp8", fn, info)
     if not a.no_stack and only in (None, "cfg4", "cfg5int8", "cfg5mxfp8"):
         from flashim_amd import blocks
 
         if only in (None, "cfg4"):
             for preset in ("mxfp8", "int8"):
                 fn, info = blocks.bench_block(preset, device=DEV)
-                ms = time_graph(fn, steps, warmup)
+                ms = time_graph(fn, steps, warmup, per_graph=2)
                 results[f"cfg4_block_{preset}"] = {
                     "ms": round(ms, 5), "GBps_unfused_chain": round(info["bytes"] / (ms * 1e-3) / 1e9, 1),
                     "hbm_frac": round(info["bytes"] / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
@@ -258,7 +283,7 @@ def main() -> int:
         for preset in ("int8", "mxfp8"):
             if only in (None, f"cfg5{preset}"):
                 fn, info = blocks.bench_stack(preset, device=DEV)
-                ms = time_graph(fn, max(3, steps // 10), max(1, warmup // 5))
+                ms = time_graph(fn, 3, 1, per_graph=1)
                 results[f"cfg5_stack_{preset}"] = {
                     "ms": round(ms, 4), "TOPS": round(info["ops"] / (ms * 1e-3) / 1e12, 2),
                     "blocks": info["blocks"], "pixels_per_scale": info["pixels"],
@@ -280,7 +305,7 @@ def main() -> int:
         "config": {"workload": "cfg2: MXFP8 1x1 conv + bias + GELU, NHWC N=2 H=W=100 Cin=Cout=512, BF16 out",
                    "M": 20000, "N": 512, "K": 512, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(achieved_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(achieved_gbs / PEAK_HBM_GBS, 4), "traffic": CFG2_TRAFFIC_BYTES,
                      "mfma_frac": round(value / PEAK_MX_TFLOPS, 4), "algorithmic_bytes": info["bytes"]},
         "configs": results,
     }

@@ -45,6 +45,7 @@ SIGNATURES: dict[str, list] = {
     "fim_test_e4m3": [_vp, _i64, _vp, _vp],
     "fim_test_mx_exponent": [_vp, _i64, _vp, _vp],
     "fim_test_bf16": [_vp, _i64, _vp, _vp],
+    "fim_test_gelu": [_vp, _i64, _vp, _vp],
 }
 
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}

@@ -11,19 +11,13 @@
 // Layout: input BF16 NHWC [B, H, W, C] (the channels-last memory of [B, C, H, W]); weight BF16 [25, C] (ky, kx major,
 // flashim/quant/passes/separable_conv_block.py:52-55); bias FP32 [C]. Output row = pixel (b, y, x), C channels.
 //
-// Work split: a lane owns 4 consecutive channels of one output column and walks TH output rows with row rolling: each
-// input row's 5 horizontal taps are loaded once and accumulated into the 5 output rows that use them (5 loads per
-// pixel instead of 25), FP32 FMA in ky-major, kx-minor order. A workgroup is 256 lanes = (CPB / 4) channel groups x
-// (1024 / CPB) columns, so a wavefront reads whole contiguous pixel runs. The 25 x 4 weights live in VGPRs.
+// Work split: see the tile comment at dw5x5_kernel. The 25 x 4 weights of a lane's channels live in VGPRs.
 #include "common.h"
 
 namespace fim {
 
 enum { ACT_RELU = 0, ACT_GELU = 1 };
 enum { DW_MX_DYNAMIC = 0, DW_INT8 = 1, DW_BF16 = 2, DW_MX_STATIC = 3 };
-
-constexpr int DW_TH = 16;
-
 
 __device__ __forceinline__ void load4_bf16(const uint16_t* p, float* v) {
   uint2 q = *reinterpret_cast<const uint2*>(p);
@@ -45,18 +39,40 @@ struct DwArgs {
   int B, H, W, C;
 };
 
-template <int CPB, int ACT, int OUT>
+// Tile: 32 output columns x 16 output rows x 32 channels per workgroup. The (16 + 4) x (32 + 4) input pixels of the
+// 32-channel slice (64 B each) are staged in LDS once; a lane then owns 4 channels of one column and walks the 20 input
+// rows with row rolling: each row's 5 horizontal taps are read from LDS once and accumulated into the 5 output rows
+// that use them, FP32 FMA in ky-major, kx-minor order (the order of a direct 25-tap loop). Lane l of a wavefront reads
+// channel quad l % 8 of column l / 8, so a tap read is 64 lanes x 8 contiguous bytes: no LDS bank conflicts.
+constexpr int DW_TW = 32, DW_TH = 16, DW_CS = 32;  // output columns, output rows, channels per workgroup
+constexpr int DW_IW = DW_TW + 4, DW_IH = DW_TH + 4;
+
+template <int ACT, int OUT>
 __global__ __launch_bounds__(256) void dw5x5_kernel(const DwArgs a) {
-  constexpr int LPP = CPB / 4;    // lanes per pixel
-  constexpr int PX = 256 / LPP;   // pixels (columns) per workgroup
+  __shared__ __attribute__((aligned(16))) uint16_t tile[DW_IH * DW_IW * DW_CS];  // [row][col][32 ch] BF16, 46 KB
   const int tid = threadIdx.x;
-  const int cl = tid % LPP;
-  const int px = tid / LPP;
-  const int x = blockIdx.x * PX + px;
+  const int x0 = blockIdx.x * DW_TW;
   const int y0 = blockIdx.y * DW_TH;
-  const int cblocks = a.C / CPB;
-  const int b = blockIdx.z / cblocks;
-  const int c = (blockIdx.z % cblocks) * CPB + cl * 4;
+  const int cslices = a.C / DW_CS;
+  const int b = blockIdx.z / cslices;
+  const int cbase = (blockIdx.z % cslices) * DW_CS;
+
+  // stage the input tile: 20 x 36 pixels x 4 segments of 16 B (8 channels), zero outside the image
+  for (int i = tid; i < DW_IH * DW_IW * 4; i += 256) {
+    const int segi = i & 3, pix = i >> 2;
+    const int r = pix / DW_IW, cidx = pix - r * DW_IW;
+    const int iy = y0 - 2 + r, ix = x0 - 2 + cidx;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (iy >= 0 && iy < a.H && ix >= 0 && ix < a.W)
+      v = *reinterpret_cast<const uint4*>(a.x + (((int64_t)b * a.H + iy) * a.W + ix) * a.C + cbase + segi * 8);
+    *reinterpret_cast<uint4*>(&tile[pix * DW_CS + segi * 8]) = v;
+  }
+
+  const int lane = tid & 63, wave = tid >> 6;
+  const int cq = lane & 7;                   // channel quad within the 32-channel slice
+  const int xl = wave * 8 + (lane >> 3);     // output column within the tile
+  const int x = x0 + xl;
+  const int c = cbase + cq * 4;
   const bool x_ok = x < a.W;
 
   float wt[25][4];
@@ -72,6 +88,10 @@ __global__ __launch_bounds__(256) void dw5x5_kernel(const DwArgs a) {
     oinv8 = __fdiv_rn(1.0f, oscale);
   }
   if (OUT == DW_MX_STATIC) oinv = exp2_int(-(int)a.expo[c >> 5]);
+  const int64_t groups = a.C >> 5;
+  const int64_t tiles_k = (groups + 3) >> 2;
+
+  __syncthreads();
 
   float acc[5][4];
 #pragma unroll
@@ -79,26 +99,14 @@ __global__ __launch_bounds__(256) void dw5x5_kernel(const DwArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[k][i] = 0.f;
 
-  const int64_t groups = a.C >> 5;
-  const int64_t tiles_k = (groups + 3) >> 2;
-
-#pragma unroll 1
-  for (int s = 0; s < DW_TH + 4; ++s) {
-    const int iy = y0 - 2 + s;
-    if (iy >= a.H + 2) break;  // uniform across the workgroup
-    const bool row_ok = iy >= 0 && iy < a.H;
+  const int rows = min(DW_TH, a.H - y0);  // output rows of this tile
+#pragma unroll 2
+  for (int s = 0; s < rows + 4; ++s) {
+    const uint16_t* rp = &tile[(s * DW_IW + xl) * DW_CS + cq * 4];
     float v[5][4];
 #pragma unroll
-    for (int kx = 0; kx < 5; ++kx) {
-      const int ix = x + kx - 2;
-      if (row_ok && x_ok && ix >= 0 && ix < a.W) {
-        load4_bf16(a.x + (((int64_t)b * a.H + iy) * a.W + ix) * a.C + c, v[kx]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[kx][i] = 0.f;
-      }
-    }
-    // output row iy + 2 - ky receives tap row ky: acc[4 - ky]
+    for (int kx = 0; kx < 5; ++kx) load4_bf16(rp + kx * DW_CS, v[kx]);
+    // output row (s - 2) + 2 - ky of the tile receives tap row ky: acc[4 - ky]
 #pragma unroll
     for (int ky = 0; ky < 5; ++ky)
 #pragma unroll
@@ -106,17 +114,21 @@ __global__ __launch_bounds__(256) void dw5x5_kernel(const DwArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[4 - ky][i] = fmaf(v[kx][i], wt[ky * 5 + kx][i], acc[4 - ky][i]);
 
-    const int oy = iy - 2;
-    if (s >= 4 && oy < a.H) {  // acc[0] holds all 25 taps of output row oy (uniform condition)
+    if (s >= 4) {  // acc[0] holds all 25 taps of tile row s - 4
+      const int oy = y0 + s - 4;
       float y[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float t = acc[0][i] + bias[i];
-        if (ACT == ACT_RELU) {
-          y[i] = fmaxf(t, 0.f);
-        } else {
-          y[i] = round_bf16(gelu_erf(round_bf16(t)));
-        }
+      for (int i = 0; i < 4; ++i) y[i] = acc[0][i] + bias[i];
+      if (ACT == ACT_RELU) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[i] = fmaxf(y[i], 0.f);
+      } else {
+        round_bf16x2(y[0], y[1]);
+        round_bf16x2(y[2], y[3]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[i] = gelu_erf(y[i]);
+        round_bf16x2(y[0], y[1]);
+        round_bf16x2(y[2], y[3]);
       }
       const int64_t row = ((int64_t)b * a.H + oy) * a.W + x;
       if (OUT == DW_MX_DYNAMIC) {
@@ -127,10 +139,10 @@ __global__ __launch_bounds__(256) void dw5x5_kernel(const DwArgs a) {
         const int e = mx_exponent_from_amax(amax);
         const float inv = exp2_int(-e);
         if (x_ok) {
-          uint32_t q = pack_e4m3x4(mx_scale_clamp(y[0], inv), mx_scale_clamp(y[1], inv), mx_scale_clamp(y[2], inv),
-                                   mx_scale_clamp(y[3], inv));
+          const uint32_t q = pack_e4m3x4(mx_scale_clamp(y[0], inv), mx_scale_clamp(y[1], inv),
+                                         mx_scale_clamp(y[2], inv), mx_scale_clamp(y[3], inv));
           *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.out) + row * a.C + c) = q;
-          if ((c & 31) == 0) {
+          if (cq == 0) {
             const int64_t gi = c >> 5;
             if (a.expo_out != nullptr) a.expo_out[row * groups + gi] = (int8_t)e;
             if (a.swizzled != nullptr) {
@@ -142,21 +154,21 @@ __global__ __launch_bounds__(256) void dw5x5_kernel(const DwArgs a) {
         }
       } else if (x_ok) {
         if (OUT == DW_INT8) {
+          if (ACT == ACT_RELU) {
+            round_bf16x2(y[0], y[1]);
+            round_bf16x2(y[2], y[3]);
+          }
           uint32_t q = 0;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float t = ACT == ACT_RELU ? round_bf16(y[i]) : y[i];
-            q |= (uint32_t)(uint8_t)quantize_int8_fast(t, oscale, oinv8) << (8 * i);
-          }
+          for (int i = 0; i < 4; ++i) q |= (uint32_t)(uint8_t)quantize_int8_fast(y[i], oscale, oinv8) << (8 * i);
           *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.out) + row * a.C + c) = q;
         } else if (OUT == DW_MX_STATIC) {
-          uint32_t q = pack_e4m3x4(mx_scale_clamp(y[0], oinv), mx_scale_clamp(y[1], oinv),
-                                   mx_scale_clamp(y[2], oinv), mx_scale_clamp(y[3], oinv));
+          const uint32_t q = pack_e4m3x4(mx_scale_clamp(y[0], oinv), mx_scale_clamp(y[1], oinv),
+                                         mx_scale_clamp(y[2], oinv), mx_scale_clamp(y[3], oinv));
           *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.out) + row * a.C + c) = q;
         } else {
-          uint32_t lo = (uint32_t)f32_to_bf16(y[0]) | ((uint32_t)f32_to_bf16(y[1]) << 16);
-          uint32_t hi = (uint32_t)f32_to_bf16(y[2]) | ((uint32_t)f32_to_bf16(y[3]) << 16);
-          *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + row * a.C + c) = make_uint2(lo, hi);
+          *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + row * a.C + c) =
+              make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
         }
       }
     }
@@ -170,13 +182,13 @@ __global__ __launch_bounds__(256) void dw5x5_kernel(const DwArgs a) {
   }
 }
 
-template <int CPB, int ACT>
+template <int ACT>
 static void dw_launch_out(const DwArgs& a, int out_mode, dim3 grid, hipStream_t s) {
   switch (out_mode) {
-    case DW_MX_DYNAMIC: dw5x5_kernel<CPB, ACT, DW_MX_DYNAMIC><<<grid, dim3(256), 0, s>>>(a); break;
-    case DW_INT8: dw5x5_kernel<CPB, ACT, DW_INT8><<<grid, dim3(256), 0, s>>>(a); break;
-    case DW_BF16: dw5x5_kernel<CPB, ACT, DW_BF16><<<grid, dim3(256), 0, s>>>(a); break;
-    default: dw5x5_kernel<CPB, ACT, DW_MX_STATIC><<<grid, dim3(256), 0, s>>>(a); break;
+    case DW_MX_DYNAMIC: dw5x5_kernel<ACT, DW_MX_DYNAMIC><<<grid, dim3(256), 0, s>>>(a); break;
+    case DW_INT8: dw5x5_kernel<ACT, DW_INT8><<<grid, dim3(256), 0, s>>>(a); break;
+    case DW_BF16: dw5x5_kernel<ACT, DW_BF16><<<grid, dim3(256), 0, s>>>(a); break;
+    default: dw5x5_kernel<ACT, DW_MX_STATIC><<<grid, dim3(256), 0, s>>>(a); break;
   }
 }
 
@@ -200,20 +212,16 @@ int fim_depthwise5x5(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t
   if (((uintptr_t)x % 8) != 0 || ((uintptr_t)weight % 8) != 0 || ((uintptr_t)out % 8) != 0) return FIM_ERR_UNSUPPORTED;
   if (B * H * W == 0) return FIM_OK;
   if (H > 2147483647LL || W > 2147483647LL) return FIM_ERR_UNSUPPORTED;
+  if (((uintptr_t)x % 16) != 0) return FIM_ERR_UNSUPPORTED;
   DwArgs a{x, weight, bias, scale, exponent, out, swizzled, exponent_out, (int)B, (int)H, (int)W, (int)C};
-  const int cpb = (C % 64 == 0) ? 64 : 32;
-  const int px = 256 / (cpb / 4);
-  const int64_t gz = B * (C / cpb);
+  const int64_t gz = B * (C / DW_CS);
   const int64_t gy = cdiv(H, DW_TH);
   if (gz > 65535 || gy > 65535) return FIM_ERR_UNSUPPORTED;
-  dim3 grid((unsigned)cdiv(W, px), (unsigned)gy, (unsigned)gz);
-  if (cpb == 64) {
-    if (act == ACT_RELU) dw_launch_out<64, ACT_RELU>(a, out_mode, grid, stream);
-    else dw_launch_out<64, ACT_GELU>(a, out_mode, grid, stream);
-  } else {
-    if (act == ACT_RELU) dw_launch_out<32, ACT_RELU>(a, out_mode, grid, stream);
-    else dw_launch_out<32, ACT_GELU>(a, out_mode, grid, stream);
-  }
+  dim3 grid((unsigned)cdiv(W, DW_TW), (unsigned)gy, (unsigned)gz);
+  if (act == ACT_RELU)
+    dw_launch_out<ACT_RELU>(a, out_mode, grid, stream);
+  else
+    dw_launch_out<ACT_GELU>(a, out_mode, grid, stream);
   return launch_status();
 }
 

@@ -17,6 +17,11 @@ __global__ void test_bf16_kernel(const float* x, int64_t n, uint16_t* out) {
   out[n + i] = f32_to_bf16(x[i]);
 }
 
+__global__ void test_gelu_kernel(const uint16_t* x, int64_t n, uint16_t* out) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = f32_to_bf16(gelu_erf(bf16_to_f32(x[i])));
+}
+
 __global__ void test_mx_exponent_kernel(const float* amax, int64_t n, int8_t* out) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) out[i] = (int8_t)mx_exponent_from_amax(amax[i]);
@@ -41,6 +46,13 @@ int fim_test_bf16(const float* x, int64_t n, uint16_t* out, hipStream_t stream) 
   if (x == nullptr || out == nullptr || n < 0) return FIM_ERR_INVALID;
   if (n == 0) return FIM_OK;
   test_bf16_kernel<<<dim3((unsigned)cdiv(n, 256)), dim3(256), 0, stream>>>(x, n, out);
+  return launch_status();
+}
+
+int fim_test_gelu(const uint16_t* x, int64_t n, uint16_t* out, hipStream_t stream) {
+  if (x == nullptr || out == nullptr || n < 0) return FIM_ERR_INVALID;
+  if (n == 0) return FIM_OK;
+  test_gelu_kernel<<<dim3((unsigned)cdiv(n, 256)), dim3(256), 0, stream>>>(x, n, out);
   return launch_status();
 }
 

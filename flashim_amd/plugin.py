@@ -1,0 +1,84 @@
+"""Registration into an installed FlashIM: the ``flashim.backends`` entry point (``flashim/backends/_loader.py:63-70``
+calls the loaded object) points here.
+
+For each op this backend implements, ``register()`` adds an impl named ``"hip"`` to FlashIM's own op object
+(``ops.<op>.register(name, device=DeviceSpec("rocm"), priority=..., when=...)``, ``flashim/ops/_registry.py:185-210``)
+with the torch reference's signature. FlashIM's ROCm platform carries no gfx950 ISA features
+(``flashim/platforms/others.py:16-30``), so the ``when`` predicates check the architecture (gfx950) and that the HIP
+library is built; on any other call FlashIM's own torch reference stays the fallback, unchanged. Results are returned as
+FlashIM's container types (``flashim.quant.tensor.QuantizedTensor`` / ``Int8Tensor``), which share this package's
+field layout.
+"""
+
+from __future__ import annotations
+
+import importlib
+import logging
+from collections.abc import Callable
+
+from flashim_amd import _lib
+from flashim_amd.backends.hip import conv as _conv
+from flashim_amd.backends.hip import quantize as _quantize
+
+logger = logging.getLogger(__name__)
+
+HIP = "hip"
+PRIORITY = 2  # above FlashIM's NVIDIA-only impls, which never match "rocm" anyway
+
+REGISTERED: list[str] = []
+
+
+def _available() -> bool:
+    return _lib.available()
+
+
+def _guard(when: Callable[..., bool]) -> Callable[..., bool]:
+    def predicate(*args, **kwargs) -> bool:
+        return _available() and bool(when(*args, **kwargs))
+
+    return predicate
+
+
+def _adapt_quantized(upstream_tensor_module):
+    def quantize_mxfp8(value, scale_exponent):
+        q = _quantize.quantize_mxfp8(value, scale_exponent)
+        return upstream_tensor_module.QuantizedTensor(q.values, q.scale_exponent, q.logical_shape)
+
+    def quantize_int8(value, scale, *, channel_scale=None):
+        q = _quantize.quantize_int8(value, scale, channel_scale=channel_scale)
+        return upstream_tensor_module.Int8Tensor(q.values, q.scale)
+
+    return quantize_mxfp8, quantize_int8
+
+
+def impls(upstream_tensor_module) -> dict[str, tuple[Callable, Callable]]:
+    """``{op name: (impl, when)}`` for the FlashIM ops this backend replaces."""
+    quantize_mxfp8, quantize_int8 = _adapt_quantized(upstream_tensor_module)
+    return {
+        "quantize_mxfp8": (quantize_mxfp8, _quantize.eligible_quantize_mxfp8),
+        "quantize_int8": (quantize_int8, _quantize.eligible_quantize_int8),
+        "int8_conv2d": (_conv.int8_conv2d, _conv.eligible_int8_conv2d),
+        "mxfp8_conv2d": (_conv.mxfp8_conv2d, _conv.eligible_mxfp8_conv2d),
+        "depthwise5x5_relu_mxfp8": (_conv.depthwise5x5_relu_mxfp8, _conv.eligible_depthwise),
+        "depthwise5x5_relu_int8": (_conv.depthwise5x5_relu_int8, _conv.eligible_depthwise),
+    }
+
+
+def register(flashim_ops=None, flashim_registry=None, flashim_tensor=None) -> list[str]:
+    """Register the HIP impls into FlashIM (modules injectable for tests). Returns the op names registered."""
+    flashim_ops = flashim_ops or importlib.import_module("flashim.ops")
+    flashim_registry = flashim_registry or importlib.import_module("flashim.ops._registry")
+    flashim_tensor = flashim_tensor or importlib.import_module("flashim.quant.tensor")
+    device = flashim_registry.DeviceSpec("rocm")
+    done = []
+    for name, (fn, when) in impls(flashim_tensor).items():
+        op = getattr(flashim_ops, name, None)
+        if op is None:
+            logger.info("FlashIM has no op %s; skipped", name)
+            continue
+        if any(impl.name == HIP for impl in getattr(op, "impls", [])):
+            continue
+        op.register(HIP, device=device, priority=PRIORITY, when=_guard(when))(fn)
+        done.append(name)
+    REGISTERED.extend(done)
+    return done

@@ -114,6 +114,9 @@ int fim_test_e4m3(const float* x, int64_t n, uint8_t* out, hipStream_t stream);
  * (out[n + i]). */
 int fim_test_bf16(const float* x, int64_t n, uint16_t* out, hipStream_t stream);
 
+/* GELU (erf form) of n BF16 values as the kernels' epilogues evaluate it, BF16 out. */
+int fim_test_gelu(const uint16_t* x, int64_t n, uint16_t* out, hipStream_t stream);
+
 /* MX exponents of n FP32 amax values with the device rule (quant/formats/mx.py:22-26). */
 int fim_test_mx_exponent(const float* amax, int64_t n, int8_t* out, hipStream_t stream);
 

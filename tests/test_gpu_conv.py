@@ -108,9 +108,7 @@ def test_int8_conv2d_epilogues(relu, gelu):
         got = ops.int8_conv2d.get("hip")(*_dev(x, weight, a_scale, w_scale, bias), *geo, relu=relu, gelu=gelu,
                                           **{k: v.to(DEV) for k, v in kwargs.items()}).cpu()
         want = ref.int8_conv2d(x, weight, a_scale, w_scale, bias, *geo, relu=relu, gelu=gelu, **kwargs)
-        if gelu:
-            # GELU's erf: the device math library and torch's CPU erf differ by about an ulp, which 1 + erf(x) turns
-            # into a large relative error where GELU's output is tiny (x < -3): compare with an absolute floor
+        if gelu:  # GELU within one BF16 rounding (or 2^-12 in torch's cancelling tail); INT8 codes within one step
             diff = (got.float() - want.float()).abs()
             if got.dtype == torch.int8:
                 assert diff.max() <= 1 and (got != want).float().mean() < 1e-3

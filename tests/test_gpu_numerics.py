@@ -68,3 +68,19 @@ def test_bf16_hardware_rounding_matches_torch():
         want = x.to(torch.bfloat16).view(torch.int16)
         assert torch.equal(out[x.numel():], want)
         assert torch.equal(out[: x.numel()], want), f"{(out[: x.numel()] != want).sum().item()} hardware BF16 mismatches"
+
+
+def test_gelu_within_one_bf16_rounding_of_torch_on_every_bf16_input():
+    """The epilogues' GELU vs F.gelu on a BF16 tensor over all finite BF16 inputs: within one BF16 rounding of
+    torch's value or an absolute 2^-12 (torch's negative tail, where 1 + erf cancels)."""
+    x = torch.arange(0, 65536, dtype=torch.int32).to(torch.int16)
+    xd = x.to(DEV)
+    out = torch.empty(65536, device=DEV, dtype=torch.int16)
+    _lib.call("fim_test_gelu", xd.data_ptr(), 65536, out.data_ptr(), _lib.stream_of(xd))
+    xs = x.view(torch.bfloat16)
+    want = torch.nn.functional.gelu(xs).float()
+    got = out.cpu().view(torch.bfloat16).float()
+    ok = torch.isfinite(xs.float()) & (xs.float().abs() < 1e30)
+    diff = (got - want).abs()[ok]
+    assert (diff <= want.abs()[ok] * 2**-7 + 2**-12).all()
+    assert (got[ok] != want[ok]).float().mean() < 0.02

@@ -1,0 +1,217 @@
+"""CPU tests of everything but the GPU compute: the C-ABI library loads and exports every symbol the header declares,
+the host build of the kernels' scalar numerics matches torch exhaustively, the op registry keeps FlashIM's dispatch
+semantics (flashim/ops/_registry.py; its tests tests/unit/test_registry.py), platform detection, the no-fallback
+rule, and the host-side layout / packing helpers."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from flashim_amd import _lib, blocks, ops, quant, registry
+from flashim_amd.platforms import Feature, Platform, rocm_features
+from oracle import reference as ref
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+# -- the C ABI ---------------------------------------------------------------------------------------------------
+
+
+def test_library_exports_every_declared_symbol():
+    header = (ROOT / "include" / "flashim_amd.h").read_text()
+    declared = set(re.findall(r"^int (fim_\w+)\(", header, re.M))
+    assert {"fim_int8_conv2d", "fim_mxfp8_conv2d", "fim_quantize_mxfp8", "fim_depthwise5x5"} <= declared
+    lib = _lib.load()
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert declared <= set(_lib.SIGNATURES), "every declared entry point has a ctypes signature"
+    assert lib.fim_version() >= 100
+
+
+def test_header_compiles_as_c():
+    import subprocess
+
+    src = '#include "flashim_amd.h"\nint main(void) { return fim_version == 0; }\n'
+    r = subprocess.run(["gcc", "-x", "c", "-std=c99", "-fsyntax-only", f"-I{ROOT / 'include'}", "-"],
+                       input=src, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def test_argument_errors_are_reported_without_a_gpu():
+    lib = _lib.load()
+    # null pointers are rejected before any launch
+    assert lib.fim_quantize_int8(None, 1, 1, 1, 1, 8, 8, 8, 8, 1, None, None, None, None) == _lib.FIM_ERR_INVALID
+    assert lib.fim_mxfp8_conv2d(*([None] + [1] * 4 + [None] * 2 + [1] + [None] * 2 + [0] + [1] * 10 + [None, 0, 0,
+                                None, None, None, None])) == _lib.FIM_ERR_INVALID
+    with pytest.raises(_lib.UnsupportedShape):
+        _lib.check(99, "x")
+    with pytest.raises(RuntimeError, match="code 7"):
+        _lib.check(7, "x")
+
+
+# -- host build of the scalar numerics ---------------------------------------------------------------------------
+
+
+def _host():
+    return _lib.load_host()
+
+
+def _call(fn, x: np.ndarray, out_dtype, *extra):
+    x = np.ascontiguousarray(x)
+    out = np.empty(x.size, dtype=out_dtype)
+    fn(x.ctypes.data_as(ctypes.c_void_p), ctypes.c_int64(x.size), *extra, out.ctypes.data_as(ctypes.c_void_p))
+    return out
+
+
+def test_host_e4m3_encoder_matches_torch():
+    h = _host()
+    bf = torch.arange(0, 65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).float()
+    bf = bf[torch.isfinite(bf)].clamp(-448, 448)
+    torch.manual_seed(0)
+    rnd = (torch.randn(1 << 20) * torch.exp2(torch.randint(-25, 10, (1 << 20,)).float())).clamp(-448, 448)
+    for x in (bf, rnd):
+        got = _call(h.fim_host_e4m3, x.numpy().astype(np.float32), np.uint8)
+        assert np.array_equal(got, x.to(torch.float8_e4m3fn).view(torch.uint8).numpy())
+    codes = np.arange(256, dtype=np.uint8)
+    dec = _call(h.fim_host_e4m3_decode, codes, np.float32)
+    want = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    finite = np.isfinite(want)
+    assert np.array_equal(dec[finite], want[finite]) and np.isnan(dec[~finite]).all()
+
+
+def test_host_mx_exponent_matches_torch_at_every_power_of_two_boundary():
+    h = _host()
+    torch.manual_seed(0)
+    ks = torch.arange(-149, 128).double()
+    bnd = (torch.exp2(ks)[:, None] * (1 + torch.arange(0, 64).double()[None] * 2.0**-23) * 448).float().flatten()
+    amax = torch.cat([torch.tensor([0.0, 448, 449, 1, 1e-30, 1e-45]), bnd, bnd.nextafter(torch.tensor(0.0)),
+                      bnd.nextafter(torch.tensor(3e38)),
+                      torch.rand(1 << 18) * torch.exp2(torch.randint(-140, 120, (1 << 18,)).float())])
+    amax = amax[torch.isfinite(amax)]
+    got = _call(h.fim_host_mx_exponent, amax.numpy(), np.int8)
+    assert np.array_equal(got, ref.scale_exponent_from_amax(amax).numpy())
+
+
+def test_host_bf16_and_int8_rounding_match_torch():
+    h = _host()
+    torch.manual_seed(0)
+    x = torch.randn(1 << 18) * torch.exp2(torch.randint(-30, 30, (1 << 18,)).float())
+    got = _call(h.fim_host_bf16, x.numpy(), np.uint16)
+    assert np.array_equal(got, x.to(torch.bfloat16).view(torch.int16).numpy().astype(np.uint16))
+    y = torch.randn(1 << 18) * 40
+    got = _call(h.fim_host_quantize_int8, y.numpy(), np.int8, ctypes.c_float(0.37))
+    assert np.array_equal(got, ref.quantize_int8_static(y, torch.tensor(0.37)).numpy())
+
+
+# -- the registry (FlashIM semantics) ----------------------------------------------------------------------------
+
+
+def _toy_op(name):
+    registry.OPS.pop(name, None)
+    op = registry.Op(name, lambda x: ("ref", x))
+    cpu = registry.DeviceSpec("cpu")
+    op.register("low", device=cpu, priority=0)(lambda x: ("low", x))
+    op.register("high", device=cpu, priority=1, when=lambda x: x > 0)(lambda x: ("high", x))
+    op.register("optin", device=cpu, priority=-1)(lambda x: ("optin", x))
+    op.register("rocm", device=registry.DeviceSpec("rocm"), requires=[Feature.HIP])(lambda x: ("rocm", x))
+    return op
+
+
+def test_registry_dispatch_order_when_optin_and_pins():
+    op = _toy_op("toy_dispatch")
+    t = torch.tensor(1.0)
+    assert op(t)[0] == "high"
+    assert op(-t)[0] == "low"  # when() rejects -> next candidate
+    assert op.get("optin")(t)[0] == "optin"  # negative priority: only pinned
+    assert op.get("reference")(t)[0] == "ref"
+    assert op.get("high")(-t)[0] == "ref"  # a pinned impl that does not apply runs the reference
+    report = op.explain(-t)
+    assert report["low"] == "selected" and report["high"] == "when() rejected the arguments"
+    assert report["rocm"].startswith("device") and report["reference"] == "fallback"
+    assert op.supports(t)
+    with pytest.raises(ValueError):
+        op.get("missing")
+    with pytest.raises(ValueError):
+        op.register("low", device=registry.DeviceSpec("cpu"))
+
+
+def test_registry_overrides_strict_mode_and_counts():
+    op = _toy_op("toy_overrides")
+    t = torch.tensor(1.0)
+    registry.configure("toy_overrides:low")
+    assert op(t)[0] == "low"
+    registry.configure("-toy_overrides")
+    assert op(t)[0] == "ref"
+    registry.configure(None)
+    with pytest.raises(ValueError):
+        registry.configure("bogus")
+    registry.reset_call_counts()
+    op(t), op(-t)
+    assert registry.call_counts()["toy_overrides"] == {"high": 1, "low": 1}
+
+
+def test_registry_bind_prepares_once():
+    registry.OPS.pop("toy_bind", None)
+    op = registry.Op("toy_bind", lambda x, w: x + w, weights=1)
+    calls = []
+    op.register("packed", device=registry.DeviceSpec("cpu"),
+                prepare=lambda w: (calls.append(1) or w * 10,))(lambda x, w: x + w)
+    bound = op.bind(torch.tensor(1.0)).warmup()
+    assert bound.primary == "packed" and len(calls) == 1
+    assert bound(torch.tensor(2.0)).item() == 12.0 and bound(torch.tensor(3.0)).item() == 13.0
+    assert len(calls) == 1
+
+
+def test_platform_features():
+    assert rocm_features("gfx950") >= {Feature.HIP, Feature.MFMA_I8, Feature.MFMA_F8F6F4_SCALED, Feature.FP8_E4M3}
+    assert Feature.HIP not in rocm_features("gfx942")  # other AMD architectures never select the gfx950 kernels
+    p = Platform("rocm", 0, arch="gfx942", features=rocm_features("gfx942"))
+    assert not registry.DeviceSpec("cuda").matches(p) and registry.DeviceSpec("rocm").matches(p)
+
+
+def test_ops_have_no_cpu_fallback():
+    """The product path computes only on the HIP kernels: on a CPU tensor every op refuses loudly."""
+    x = torch.randint(-127, 127, (1, 4, 4, 16), dtype=torch.int8)
+    w = torch.randint(-127, 127, (8, 9 * 16), dtype=torch.int8)
+    with pytest.raises(NotImplementedError, match="no HIP impl"):
+        ops.int8_conv2d(x, w, torch.tensor(0.1), torch.ones(8), None, 3, 3, 1, 1, 1, 1, 1, 1)
+    with pytest.raises(NotImplementedError):
+        ops.quantize_mxfp8(torch.randn(4, 32), torch.zeros(1, dtype=torch.int8))
+    with pytest.raises(RuntimeError, match="GPU only"):
+        quant.quantize_static(torch.randn(4, 32), torch.zeros(1, dtype=torch.int8))
+    assert ops.int8_conv2d.explain(x, w, torch.tensor(0.1), torch.ones(8), None, 3, 3, 1, 1, 1, 1, 1, 1)["hip"]
+
+
+# -- host-side layout and packing helpers ------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("rows,groups", [(1, 1), (300, 32), (130, 5)])
+def test_swizzle_layout_helpers_match_oracle(rows, groups):
+    e = torch.randint(-20, 10, (rows, groups), dtype=torch.int8)
+    sw = quant.swizzle_scales(e)
+    assert torch.equal(sw.view(torch.uint8), ref.swizzle_scales(e))
+    assert torch.equal(quant.unswizzle_scales(sw, rows, groups), e)
+    assert quant.swizzled_size(rows, groups) == sw.numel()
+
+
+def test_block_batchnorm_fold_matches_torch_fusion():
+    g = torch.Generator().manual_seed(0)
+    wts = blocks.BlockWeights.random(32, g, "cpu")
+    conv = torch.nn.Conv2d(32, 32, 5, padding=2, groups=32).eval()
+    bn = torch.nn.BatchNorm2d(32, eps=blocks.BN_EPS).eval()
+    with torch.no_grad():
+        conv.weight.copy_(wts.dw_weight), conv.bias.copy_(wts.dw_bias)
+        bn.weight.copy_(wts.bn_gamma), bn.bias.copy_(wts.bn_beta)
+        bn.running_mean.copy_(wts.bn_mean), bn.running_var.copy_(wts.bn_var)
+    fused = torch.nn.utils.fusion.fuse_conv_bn_eval(conv, bn)
+    packed, bias = wts.folded_depthwise()
+    want = fused.weight.detach()[:, 0].permute(1, 2, 0).reshape(25, 32).to(torch.bfloat16)
+    assert torch.equal(packed, want)
+    assert torch.allclose(bias, fused.bias.detach(), rtol=1e-6, atol=1e-7)
+    x = torch.randn(1, 32, 6, 7)
+    assert torch.allclose(F.conv2d(x, fused.weight, fused.bias, padding=2, groups=32), bn(conv(x)), atol=1e-5)
