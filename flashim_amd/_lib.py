@@ -41,6 +41,11 @@ SIGNATURES: dict[str, list] = {
         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
         _vp, _i32, _i64, _vp, _vp, _vp, _vp,
     ],
+    "fim_int8_linear": [
+        _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _i64, _i64, _vp, _vp, _vp,
+    ],
+    "fim_mxfp8_scaled_mm": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i32, _vp, _vp],
+    "fim_im2col_gather": [_vp, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp],
     "fim_depthwise5x5": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp],
     "fim_test_e4m3": [_vp, _i64, _vp, _vp],
     "fim_test_mx_exponent": [_vp, _i64, _vp, _vp],

@@ -196,3 +196,66 @@ def eligible_depthwise(value: Tensor, weight: Tensor, bias: Tensor, *rest, **kwa
         and tuple(weight.shape) == (25, value.shape[1]) and tuple(bias.shape) == (value.shape[1],)
         and (kwargs.get("exponent") is None or kwargs["exponent"].numel() == value.shape[1] // 32)
     )
+
+
+# -- im2col and the depthwise-then-pointwise composites ------------------------------------------------------------
+
+
+def im2col_gather(x: Tensor, kh: int, kw: int, sh: int, sw: int, ph: int, pw: int, dh: int, dw: int) -> Tensor:
+    """``x`` ``[B, H, W, C]`` of a 1-byte dtype -> ``[B*Ho*Wo, kh*kw*C]`` in (ky, kx, c) order, zero padding."""
+    b, h, w, c = x.shape
+    ho, wo = conv_output_size(h, w, kh, kw, sh, sw, ph, pw, dh, dw)
+    x = x.contiguous()
+    out = torch.empty(b * ho * wo, kh * kw * c, device=x.device, dtype=x.dtype)
+    _lib.call("fim_im2col_gather", x.view(torch.uint8).data_ptr(), b, h, w, c, kh, kw, sh, sw, ph, pw, dh, dw,
+              out.view(torch.uint8).data_ptr(), _lib.stream_of(x), what="im2col_gather")
+    return out
+
+
+def depthwise5x5_relu_pointwise_mxfp8(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
+                                      pw_scale_swizzled: Tensor, pw_scale_u8: Tensor, pw_bias: Tensor) -> Tensor:
+    """The MXFP8 refiner block (``flashim/ops/conv.py:93-113``): depthwise producer (dynamic MXFP8) then the
+    block-scaled pointwise GEMM with the weight's plain E8M0 bytes; ``[B, C, H, W]`` view of NHWC BF16."""
+    from flashim_amd.backends.hip import gemm
+
+    batch, channels, height, width = value.shape
+    quantized, scale = depthwise5x5_relu_mxfp8(value, dw_weight, dw_bias)
+    n, k = pw_weight.shape
+    w_exponent = (pw_scale_u8.view(torch.uint8).to(torch.int16) - 127).to(torch.int8).reshape(n, k // 32)
+    m = quantized.shape[0]
+    bias, bias_code = gemm._bias(pw_bias, value.device)
+    out = torch.empty(m, n, device=value.device, dtype=torch.bfloat16)
+    _lib.call("fim_mxfp8_scaled_mm", quantized.data_ptr(), m, k, scale.view(torch.uint8).data_ptr(),
+              pw_weight.contiguous().view(torch.uint8).data_ptr(), n, w_exponent.contiguous().data_ptr(),
+              _lib.ptr(bias), bias_code, out.data_ptr(), _lib.stream_of(value), what="pointwise mxfp8")
+    return out.reshape(batch, height, width, n).permute(0, 3, 1, 2)
+
+
+def depthwise5x5_relu_pointwise_int8(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
+                                     pw_wscale: Tensor, pw_bias: Tensor, scale: Tensor) -> Tensor:
+    """The INT8 refiner block (``flashim/ops/conv.py:119-138``): static INT8 producer then ``int8_linear``."""
+    from flashim_amd.backends.hip import gemm
+
+    batch, channels, height, width = value.shape
+    quantized = depthwise5x5_relu_int8(value, dw_weight, dw_bias, scale)
+    out = gemm.int8_linear(quantized, pw_weight, scale, pw_wscale, pw_bias)
+    return out.reshape(batch, height, width, -1).permute(0, 3, 1, 2)
+
+
+def eligible_im2col(x, kh, kw, sh, sw, ph, pw, dh, dw) -> bool:
+    return isinstance(x, Tensor) and is_gfx950(x.device) and x.ndim == 4 and x.element_size() == 1
+
+
+def eligible_pointwise_mxfp8(value, dw_weight, dw_bias, pw_weight, pw_scale_swizzled, pw_scale_u8, pw_bias) -> bool:
+    return (
+        eligible_depthwise(value, dw_weight, dw_bias) and pw_weight.dtype == torch.float8_e4m3fn
+        and pw_weight.ndim == 2 and pw_weight.shape[1] == value.shape[1]
+        and pw_scale_u8.numel() == pw_weight.shape[0] * pw_weight.shape[1] // 32
+    )
+
+
+def eligible_pointwise_int8(value, dw_weight, dw_bias, pw_weight, pw_wscale, pw_bias, scale) -> bool:
+    return (
+        eligible_depthwise(value, dw_weight, dw_bias) and pw_weight.dtype == torch.int8 and pw_weight.ndim == 2
+        and pw_weight.shape[1] == value.shape[1] and pw_wscale.numel() == pw_weight.shape[0] and scale.numel() == 1
+    )

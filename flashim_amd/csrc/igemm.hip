@@ -38,6 +38,9 @@ struct ConvArgs {
   const uint8_t* w;        // [Cout, T*Cin]
   const int8_t* x_expo;    // MX: [Cin / 32]
   const int8_t* w_expo;    // MX: [Cout, T*Cin / 32]
+  const uint8_t* x_swz;    // MX, per-row scales (XS = 1): E8M0 bytes of x in the 128x4 swizzled layout
+  int x_swz_tiles_k;       //   ceil((Cin / 32) / 4)
+  const float* a_scale_rows;  // INT8: per-row activation scales [M] (null: the per-tensor a_scale)
   const float* a_scale;    // INT8: scalar
   const float* w_scale;    // INT8: [Cout]
   const void* bias;        // [Cout] or null
@@ -48,7 +51,7 @@ struct ConvArgs {
   const float* out_scale;  // OUT_INT8
   const int8_t* out_expo;  // OUT_E4M3: [Cout / 32]
   void* out;               // [B, Ho, Wo, Cout]
-  int out_mode, relu, gelu;
+  int out_mode, relu_pre, relu_post, gelu;  // ReLU before the BF16 rounding / after the residual add
   int B, H, W, Cin, Ho, Wo, Cout;
   int kh, kw, sh, sw, ph, pw, dh, dw;
   int M;                   // output pixels (< 2^31)
@@ -97,8 +100,9 @@ __device__ __forceinline__ uint4 load_seg(const uint8_t* p, bool row_ok, int cva
   return v;
 }
 
-template <int KIND, int BN, int LW, int OUT>
+template <int KIND, int BN, int LW, int OUT, int XS>
 __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
+  constexpr int SXN = XS ? 4 : 1;        // activation scale registers per set: one per 16-pixel block with row scales
   constexpr int NB = BN / 32;            // 16-channel blocks per wavefront (BN/2 channels)
   constexpr int MB = 4;                  // 16-pixel blocks per wavefront (64 pixels)
   constexpr int A_PASSES = BM / 32;      // 256 lanes x 16 B cover 32 rows x 128 B per pass
@@ -126,7 +130,8 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
   if (tid < BN) {
     const int n = n0 + tid;
     const bool nok = n < a.Cout;
-    ep_scale[tid] = (KIND == KIND_INT8 && nok) ? *a.a_scale * a.w_scale[n] : 1.0f;
+    ep_scale[tid] = (KIND == KIND_INT8 && nok) ? (a.a_scale_rows != nullptr ? a.w_scale[n] : *a.a_scale * a.w_scale[n])
+                                               : 1.0f;
     float bias = 0.0f;
     if (a.bias != nullptr && nok)
       bias = a.bias_dtype == FIM_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(a.bias)[n])
@@ -200,14 +205,16 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
   // two register sets: the loads of step kt + 2 are issued while step kt + 1 (loaded one step earlier) waits in the
   // other set to be staged, so each load has two steps of MFMA work to land behind
   uint4 ra0[A_PASSES], rb0[B_PASSES], ra1[A_PASSES], rb1[B_PASSES];
-  int sx0 = 0, sw0[NB], sx1 = 0, sw1[NB];
+  int sx0[SXN], sw0[NB], sx1[SXN], sw1[NB];
+#pragma unroll
+  for (int j = 0; j < SXN; ++j) sx0[j] = sx1[j] = 0;
   bool bok0 = true, bok1 = true;  // the set's channel block lies inside Cin (else zero data, scale 2^0)
 #pragma unroll
   for (int i = 0; i < NB; ++i) sw0[i] = sw1[i] = 0;
 
   // (tap, channel chunk) of the step being loaded; advanced uniformly
   int ld_ky = 0, ld_kx = 0, ld_c0 = 0;
-  auto gload = [&](uint4 (&ra)[A_PASSES], uint4 (&rb)[B_PASSES], int& pre_sx, int (&pre_sw)[NB], bool& pre_ok) {
+  auto gload = [&](uint4 (&ra)[A_PASSES], uint4 (&rb)[B_PASSES], int (&pre_sx)[SXN], int (&pre_sw)[NB], bool& pre_ok) {
     const int dy = ld_ky * a.dh, dx = ld_kx * a.dw;
     const int64_t delta = (int64_t)(dy * a.W + dx) * a.Cin + ld_c0;
     const int cvalid = a.Cin - ld_c0 - seg * 16;
@@ -224,7 +231,18 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
       // computed: consuming them here would make the compiler wait for every load issued so far
       const int blk = (ld_c0 >> 5) + g;
       const int cblk = blk < cblocks ? blk : cblocks - 1;
-      pre_sx = (int)a.x_expo[cblk];
+      if (XS == 0) {
+        pre_sx[0] = (int)a.x_expo[cblk];
+      } else {
+#pragma unroll
+        for (int j = 0; j < SXN; ++j) {
+          int r = m0 + wm * 64 + j * 16 + (lane & 15);
+          r = r < a.M ? r : a.M - 1;
+          const int rt = r & 127;
+          pre_sx[j] = (int)a.x_swz[(((int64_t)(r >> 7) * a.x_swz_tiles_k + (cblk >> 2)) << 9) + (rt & 31) * 16 +
+                                   (rt >> 5) * 4 + (cblk & 3)];
+        }
+      }
       pre_ok = blk < cblocks;
       const int wblk = (ld_ky * a.kw + ld_kx) * cblocks + cblk;
 #pragma unroll
@@ -266,8 +284,10 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
 
   // one K step from LDS stage `buf`; (rsx, rsw): the raw exponent bytes loaded with it; blk_ok false marks a
   // channel block past Cin (zero data: any scale works, use 2^0)
-  auto compute = [&](int buf, int rsx, const int (&rsw)[NB], bool blk_ok) {
-    const int sx = blk_ok ? rsx + 127 : 127;
+  auto compute = [&](int buf, const int (&rsx)[SXN], const int (&rsw)[NB], bool blk_ok) {
+    int sxs[MB];
+#pragma unroll
+    for (int j = 0; j < MB; ++j) sxs[j] = !blk_ok ? 127 : XS ? rsx[j] : rsx[0] + 127;
     int sw[NB];
 #pragma unroll
     for (int i = 0; i < NB; ++i) sw[i] = blk_ok ? rsw[i] + 127 : 127;
@@ -290,7 +310,8 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
         } else {
           const v8i wf = v8i{wlo[0], wlo[1], wlo[2], wlo[3], whi[0], whi[1], whi[2], whi[3]};
           const v8i xf = v8i{xlo[j][0], xlo[j][1], xlo[j][2], xlo[j][3], xhi[j][0], xhi[j][1], xhi[j][2], xhi[j][3]};
-          acc_f[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf, xf, acc_f[i][j], 0, 0, 0, sw[i], 0, sx);
+          acc_f[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf, xf, acc_f[i][j], 0, 0, 0, sw[i], 0,
+                                                                         sxs[j]);
         }
       }
     }
@@ -300,8 +321,10 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
   for (int kt = 0; kt < nk; kt += 2) {
     // even step kt (LDS stage 0, scales in set 0); set 0 is free once staged: load step kt + 2 into it
     {
-      int sx = sx0, sw[NB];
+      int sx[SXN], sw[NB];
       const bool bok = bok0;
+#pragma unroll
+      for (int j = 0; j < SXN; ++j) sx[j] = sx0[j];
 #pragma unroll
       for (int i = 0; i < NB; ++i) sw[i] = sw0[i];
 #ifndef FIM_EXP_NOLOAD
@@ -315,8 +338,10 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
       lds_barrier();
     }
     if (kt + 1 < nk) {  // odd step kt + 1 (LDS stage 1, set 1); then stage step kt + 2 from set 0
-      int sx = sx1, sw[NB];
+      int sx[SXN], sw[NB];
       const bool bok = bok1;
+#pragma unroll
+      for (int j = 0; j < SXN; ++j) sx[j] = sx1[j];
 #pragma unroll
       for (int i = 0; i < NB; ++i) sw[i] = sw1[i];
 #ifndef FIM_EXP_NOLOAD
@@ -339,7 +364,8 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
   const float out_inv = OUT == OUT_INT8 ? __fdiv_rn(1.0f, out_scale) : 1.0f;
   const bool has_bias = a.bias != nullptr;
   const bool res = a.residual != nullptr;
-  const bool relu_pre = a.relu && !res;
+  const bool relu_pre = a.relu_pre != 0;
+  const bool relu_post = a.relu_post != 0;
   const bool res_vec = res && a.res_dtype == FIM_BF16 && a.rs_c == 1 && (((uintptr_t)a.residual) & 7) == 0 &&
                        (a.rs_w % 4) == 0 && (a.rs_h % 4) == 0 && (a.rs_b % 4) == 0;
   const bool out_vec = (a.Cout % 4) == 0;
@@ -374,8 +400,14 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
       const int m = pm[j];
       if (!any || m >= a.M) continue;
       float y[4];
+      if (KIND == KIND_INT8 && a.a_scale_rows != nullptr) {
+        const float arow = a.a_scale_rows[m];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) y[v] = KIND == KIND_INT8 ? __fmul_rn((float)acc_i[i][j][v], cs[v]) : acc_f[i][j][v];
+        for (int v = 0; v < 4; ++v) y[v] = __fmul_rn((float)acc_i[i][j][v], __fmul_rn(arow, cs[v]));
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) y[v] = KIND == KIND_INT8 ? __fmul_rn((float)acc_i[i][j][v], cs[v]) : acc_f[i][j][v];
+      }
       if (has_bias) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) y[v] = __fadd_rn(y[v], cb[v]);
@@ -402,7 +434,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
           rv[3] = u2f(pk.y & 0xffff0000u);
 #pragma unroll
           for (int v = 0; v < 4; ++v) y[v] = __fadd_rn(y[v], rv[v]);
-          if (a.relu) {
+          if (relu_post) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) y[v] = fmaxf(y[v], 0.0f);
           }
@@ -417,9 +449,9 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
               const float r = a.res_dtype == FIM_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(a.residual)[off])
                                                       : static_cast<const float*>(a.residual)[off];
               float t = __fadd_rn(y[v], r);
-              if (a.relu) t = fmaxf(t, 0.0f);
+              if (relu_post) t = fmaxf(t, 0.0f);
               y[v] = round_bf16(t);
-            } else if (a.relu) {
+            } else if (relu_post) {
               y[v] = fmaxf(y[v], 0.0f);
             }
           }
@@ -465,21 +497,32 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
   FIM_STAMP(3);
 }
 
-template <int KIND, int BN, int OUT>
+template <int KIND, int BN, int OUT, int XS>
 static void launch_lw(const ConvArgs& a, int lw, dim3 grid, hipStream_t stream) {
   if (lw == 16)
-    conv_igemm_kernel<KIND, BN, 16, OUT><<<grid, dim3(256), 0, stream>>>(a);
+    conv_igemm_kernel<KIND, BN, 16, OUT, XS><<<grid, dim3(256), 0, stream>>>(a);
   else
-    conv_igemm_kernel<KIND, BN, 1, OUT><<<grid, dim3(256), 0, stream>>>(a);
+    conv_igemm_kernel<KIND, BN, 1, OUT, XS><<<grid, dim3(256), 0, stream>>>(a);
 }
 
-template <int KIND, int BN>
+template <int KIND, int BN, int XS>
 static void launch_bn(const ConvArgs& a, int lw, dim3 grid, hipStream_t stream) {
   constexpr int QOUT = KIND == KIND_INT8 ? OUT_INT8 : OUT_E4M3;
   if (a.out_mode == OUT_BF16)
-    launch_lw<KIND, BN, OUT_BF16>(a, lw, grid, stream);
+    launch_lw<KIND, BN, OUT_BF16, XS>(a, lw, grid, stream);
   else
-    launch_lw<KIND, BN, QOUT>(a, lw, grid, stream);
+    launch_lw<KIND, BN, QOUT, XS>(a, lw, grid, stream);
+}
+
+template <int KIND, int BN>
+static void launch_xs(const ConvArgs& a, int lw, dim3 grid, hipStream_t stream) {
+  if constexpr (KIND == KIND_MX) {
+    if (a.x_swz != nullptr) {
+      launch_bn<KIND, 64, 1>(a, lw, grid, stream);  // row scales take 8 more VGPRs: the 64-channel tile keeps them
+      return;
+    }
+  }
+  launch_bn<KIND, BN, 0>(a, lw, grid, stream);
 }
 
 template <int KIND>
@@ -495,7 +538,7 @@ static int launch_conv(ConvArgs a, hipStream_t stream) {
   if (M >= (1LL << 31) - 256) return FIM_ERR_UNSUPPORTED;
   a.M = (int)M;
   a.kchunks = (a.Cin + KC - 1) / KC;
-  const int bn = a.Cout > 64 ? 128 : 64;
+  const int bn = (a.Cout > 64 && a.x_swz == nullptr) ? 128 : 64;
   a.n_tiles = (a.Cout + bn - 1) / bn;
   const int64_t m_tiles = (a.M + BM - 1) / BM;
   const int64_t tiles = m_tiles * a.n_tiles;
@@ -506,9 +549,9 @@ static int launch_conv(ConvArgs a, hipStream_t stream) {
   if (a.Cin % 16 == 0 && both % 16 == 0) lw = 16;
   dim3 grid((unsigned)(cdiv(tiles, 8) * 8));  // a multiple of the 8 XCDs: the kernel maps pids to tiles per XCD
   if (bn == 128)
-    launch_bn<KIND, 128>(a, lw, grid, stream);
+    launch_xs<KIND, 128>(a, lw, grid, stream);
   else
-    launch_bn<KIND, 64>(a, lw, grid, stream);
+    launch_xs<KIND, 64>(a, lw, grid, stream);
   return launch_status();
 }
 
@@ -519,7 +562,8 @@ static void fill_geometry(ConvArgs& a, int64_t B, int64_t H, int64_t W, int64_t 
 }
 
 static void fill_epilogue(ConvArgs& a, const void* bias, int bias_dtype, const void* residual, int res_dtype,
-                          int64_t res_channels, const int64_t* res_strides, int relu, int gelu, void* out) {
+                          int64_t res_channels, const int64_t* res_strides, int relu, int gelu, void* out,
+                          int relu_before_residual = 0) {
   a.bias = bias; a.bias_dtype = bias_dtype;
   a.residual = residual; a.res_dtype = res_dtype; a.res_channels = res_channels;
   if (residual != nullptr && res_strides != nullptr) {
@@ -527,7 +571,11 @@ static void fill_epilogue(ConvArgs& a, const void* bias, int bias_dtype, const v
   } else {
     a.rs_b = a.rs_h = a.rs_w = a.rs_c = 0;
   }
-  a.relu = relu; a.gelu = gelu; a.out = out;
+  // conv semantics (ops/conv.py:193-203): ReLU before the BF16 rounding without a residual, after the residual add
+  // with one; linear semantics (ops/gemm.py:91-97, relu_before_residual): always before, the residual added after
+  a.relu_pre = relu && (residual == nullptr || relu_before_residual);
+  a.relu_post = relu && residual != nullptr && !relu_before_residual;
+  a.gelu = gelu; a.out = out;
 }
 
 static bool dims_fit(int64_t B, int64_t H, int64_t W, int64_t Cin, int64_t Cout) {
@@ -584,4 +632,111 @@ int fim_mxfp8_conv2d(const uint8_t* x, int64_t B, int64_t H, int64_t W, int64_t 
   return launch_conv<KIND_MX>(a, stream);
 }
 
+// INT8 GEMM [M, K] x [N, K]^T with int8_linear's epilogue (ops/gemm.py:78-98): a 1x1 conv over a 1 x M "image".
+// a_scale_rows (may be null) holds per-row activation scales [M] in place of the per-tensor a_scale; ReLU comes
+// before the BF16 rounding and the residual ([M, res_channels], row stride res_row_stride) is added after it.
+int fim_int8_linear(const int8_t* a, int64_t M, int64_t K, const int8_t* weight, int64_t N, const float* a_scale,
+                    const float* a_scale_rows, const float* w_scale, const void* bias, int bias_dtype, int relu, int gelu,
+                    const void* residual, int res_dtype, int64_t res_channels, int64_t res_row_stride,
+                    const float* out_scale, void* out, hipStream_t stream) {
+  if (a == nullptr || weight == nullptr || (a_scale == nullptr && a_scale_rows == nullptr) || w_scale == nullptr ||
+      out == nullptr)
+    return FIM_ERR_INVALID;
+  if (!dims_fit(1, 1, M, K, N)) return FIM_ERR_UNSUPPORTED;
+  ConvArgs c = {};
+  c.x = reinterpret_cast<const uint8_t*>(a);
+  c.w = reinterpret_cast<const uint8_t*>(weight);
+  c.a_scale = a_scale != nullptr ? a_scale : a_scale_rows;
+  c.a_scale_rows = a_scale_rows;
+  c.w_scale = w_scale;
+  fill_geometry(c, 1, 1, M, K, N, 1, 1, 1, 1, 0, 0, 1, 1);
+  const int64_t strides[4] = {0, 0, res_row_stride, 1};
+  fill_epilogue(c, bias, bias_dtype, residual, res_dtype, res_channels, strides, relu, gelu, out, 1);
+  c.out_scale = out_scale;
+  c.out_mode = out_scale != nullptr ? OUT_INT8 : OUT_BF16;
+  return launch_conv<KIND_INT8>(c, stream);
+}
+
+// Block-scaled MXFP8 GEMM with per-(row, 32) scales on both operands (ops/gemm.py:40-49, F.scaled_mm's MXFP8 mode):
+// a [M, K] E4M3 with its E8M0 scales in the 128x4 swizzled layout (a_scale_swizzled), weight [N, K] E4M3 with int8
+// exponents [N, K/32]; out BF16 [M, N] = a @ weight^T (+ bias).
+int fim_mxfp8_scaled_mm(const uint8_t* a, int64_t M, int64_t K, const uint8_t* a_scale_swizzled,
+                        const uint8_t* weight, int64_t N, const int8_t* weight_exponent, const void* bias,
+                        int bias_dtype, void* out, hipStream_t stream) {
+  if (a == nullptr || a_scale_swizzled == nullptr || weight == nullptr || weight_exponent == nullptr || out == nullptr)
+    return FIM_ERR_INVALID;
+  if (K % 32 != 0) return FIM_ERR_UNSUPPORTED;
+  if (!dims_fit(1, 1, M, K, N)) return FIM_ERR_UNSUPPORTED;
+  ConvArgs c = {};
+  c.x = a;
+  c.w = weight;
+  c.x_expo = weight_exponent;  // unused with row scales; any valid pointer
+  c.x_swz = a_scale_swizzled;
+  c.x_swz_tiles_k = (int)(((K / 32) + 3) / 4);
+  c.w_expo = weight_exponent;
+  fill_geometry(c, 1, 1, M, K, N, 1, 1, 1, 1, 0, 0, 1, 1);
+  fill_epilogue(c, bias, bias_dtype, nullptr, 0, 0, nullptr, 0, 0, out);
+  c.out_mode = OUT_BF16;
+  return launch_conv<KIND_MX>(c, stream);
+}
+
 }  // extern "C"
+
+// ----- im2col gather (byte tensors) ----------------------------------------------------------------------------
+
+namespace fim {
+
+// [B, H, W, C] bytes -> [B*Ho*Wo, T*C] in (ky, kx, c) order, zero padding (ops/conv.py:144-165). One lane per 16
+// bytes of a (pixel, tap) segment when C % 16 == 0, else per byte.
+template <int VEC>
+__global__ __launch_bounds__(256) void im2col_kernel(const uint8_t* __restrict__ x, uint8_t* __restrict__ out, int B,
+                                                     int H, int W, int C, int Ho, int Wo, int kh, int kw, int sh,
+                                                     int sw, int ph, int pw, int dh, int dw) {
+  const int64_t segs = C / VEC;
+  const int64_t per_row = (int64_t)kh * kw * segs;
+  const int64_t total = (int64_t)B * Ho * Wo * per_row;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t m = i / per_row;
+    const int64_t rest = i - m * per_row;
+    const int tap = (int)(rest / segs);
+    const int sg = (int)(rest - (int64_t)tap * segs);
+    const int ow = (int)(m % Wo);
+    const int64_t q = m / Wo;
+    const int oh = (int)(q % Ho);
+    const int b = (int)(q / Ho);
+    const int ky = tap / kw, kx = tap - ky * kw;
+    const int ih = oh * sh - ph + ky * dh, iw = ow * sw - pw + kx * dw;
+    const bool ok = ih >= 0 && ih < H && iw >= 0 && iw < W;
+    const uint8_t* src = x + (((int64_t)b * H + ih) * W + iw) * C + (int64_t)sg * VEC;
+    uint8_t* dst = out + i * VEC;
+    if (VEC == 16) {
+      *reinterpret_cast<uint4*>(dst) = ok ? *reinterpret_cast<const uint4*>(src) : make_uint4(0, 0, 0, 0);
+    } else {
+      *dst = ok ? *src : (uint8_t)0;
+    }
+  }
+}
+
+}  // namespace fim
+
+extern "C" int fim_im2col_gather(const uint8_t* x, int64_t B, int64_t H, int64_t W, int64_t C, int kh, int kw, int sh,
+                                 int sw, int ph, int pw, int dh, int dw, uint8_t* out, hipStream_t stream) {
+  if (x == nullptr || out == nullptr || B < 0 || H < 0 || W < 0 || C <= 0 || kh <= 0 || kw <= 0 || sh <= 0 ||
+      sw <= 0 || dh <= 0 || dw <= 0 || ph < 0 || pw < 0)
+    return FIM_ERR_INVALID;
+  if (!dims_fit(B, H, W, C, 1)) return FIM_ERR_UNSUPPORTED;
+  const int Ho = (int)((H + 2 * ph - dh * (kh - 1) - 1) / sh + 1), Wo = (int)((W + 2 * pw - dw * (kw - 1) - 1) / sw + 1);
+  if (Ho <= 0 || Wo <= 0) return FIM_ERR_INVALID;
+  const bool vec = C % 16 == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)out % 16) == 0;
+  const int64_t elems = B * Ho * Wo * (int64_t)kh * kw * (vec ? C / 16 : C);
+  if (elems == 0) return FIM_OK;
+  int64_t blocks = cdiv(elems, 256);
+  if (blocks > 65536) blocks = 65536;
+  if (vec)
+    im2col_kernel<16><<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(x, out, (int)B, (int)H, (int)W, (int)C, Ho, Wo,
+                                                                          kh, kw, sh, sw, ph, pw, dh, dw);
+  else
+    im2col_kernel<1><<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(x, out, (int)B, (int)H, (int)W, (int)C, Ho, Wo,
+                                                                         kh, kw, sh, sw, ph, pw, dh, dw);
+  return launch_status();
+}

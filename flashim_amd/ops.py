@@ -10,6 +10,7 @@ instead of computing on another path.
 from __future__ import annotations
 
 from flashim_amd.backends.hip import conv as _conv
+from flashim_amd.backends.hip import gemm as _gemm
 from flashim_amd.backends.hip import quantize as _quantize
 from flashim_amd.platforms import Feature
 from flashim_amd.registry import (  # noqa: F401  (re-exported API)
@@ -23,6 +24,12 @@ int8_conv2d = Op("int8_conv2d", composite=True)
 mxfp8_conv2d = Op("mxfp8_conv2d", composite=True)
 depthwise5x5_relu_mxfp8 = Op("depthwise5x5_relu_mxfp8")
 depthwise5x5_relu_int8 = Op("depthwise5x5_relu_int8")
+depthwise5x5_relu_pointwise_mxfp8 = Op("depthwise5x5_relu_pointwise_mxfp8", composite=True)
+depthwise5x5_relu_pointwise_int8 = Op("depthwise5x5_relu_pointwise_int8", composite=True)
+im2col_gather = Op("im2col_gather")
+int8_linear = Op("int8_linear")
+mxfp8_linear = Op("mxfp8_linear", weights=1)
+mxfp8_scaled_mm = Op("mxfp8_scaled_mm")
 # this backend's refiner-block producer (folded BatchNorm + GELU)
 depthwise5x5_gelu = Op("depthwise5x5_gelu")
 
@@ -39,6 +46,15 @@ IMPLS = (
      _conv.eligible_depthwise),
     ("depthwise5x5_relu_int8", _conv.depthwise5x5_relu_int8, (Feature.HIP,), _conv.eligible_depthwise),
     ("depthwise5x5_gelu", _conv.depthwise5x5_gelu, (Feature.HIP,), _conv.eligible_depthwise),
+    ("depthwise5x5_relu_pointwise_mxfp8", _conv.depthwise5x5_relu_pointwise_mxfp8,
+     (Feature.HIP, Feature.MFMA_F8F6F4_SCALED), _conv.eligible_pointwise_mxfp8),
+    ("depthwise5x5_relu_pointwise_int8", _conv.depthwise5x5_relu_pointwise_int8, (Feature.HIP, Feature.MFMA_I8),
+     _conv.eligible_pointwise_int8),
+    ("im2col_gather", _conv.im2col_gather, (Feature.HIP,), _conv.eligible_im2col),
+    ("int8_linear", _gemm.int8_linear, (Feature.HIP, Feature.MFMA_I8), _gemm.eligible_int8_linear),
+    ("mxfp8_linear", _gemm.mxfp8_linear, (Feature.HIP, Feature.MFMA_F8F6F4_SCALED), _gemm.eligible_mxfp8_linear),
+    ("mxfp8_scaled_mm", _gemm.mxfp8_scaled_mm, (Feature.HIP, Feature.MFMA_F8F6F4_SCALED),
+     _gemm.eligible_mxfp8_scaled_mm),
 )
 
 for _name, _fn, _requires, _when in IMPLS:

@@ -18,6 +18,7 @@ from collections.abc import Callable
 
 from flashim_amd import _lib
 from flashim_amd.backends.hip import conv as _conv
+from flashim_amd.backends.hip import gemm as _gemm
 from flashim_amd.backends.hip import quantize as _quantize
 
 logger = logging.getLogger(__name__)
@@ -61,6 +62,12 @@ def impls(upstream_tensor_module) -> dict[str, tuple[Callable, Callable]]:
         "mxfp8_conv2d": (_conv.mxfp8_conv2d, _conv.eligible_mxfp8_conv2d),
         "depthwise5x5_relu_mxfp8": (_conv.depthwise5x5_relu_mxfp8, _conv.eligible_depthwise),
         "depthwise5x5_relu_int8": (_conv.depthwise5x5_relu_int8, _conv.eligible_depthwise),
+        "depthwise5x5_relu_pointwise_mxfp8": (_conv.depthwise5x5_relu_pointwise_mxfp8,
+                                              _conv.eligible_pointwise_mxfp8),
+        "depthwise5x5_relu_pointwise_int8": (_conv.depthwise5x5_relu_pointwise_int8, _conv.eligible_pointwise_int8),
+        "im2col_gather": (_conv.im2col_gather, _conv.eligible_im2col),
+        "int8_linear": (_gemm.int8_linear, _gemm.eligible_int8_linear),
+        "mxfp8_scaled_mm": (_gemm.mxfp8_scaled_mm, _gemm.eligible_mxfp8_scaled_mm),
     }
 
 

@@ -91,6 +91,27 @@ int fim_mxfp8_conv2d(const uint8_t* x, int64_t B, int64_t H, int64_t W, int64_t 
                      const void* residual, int res_dtype, int64_t res_channels, const int64_t* res_strides,
                      const int8_t* out_exponent, void* out, hipStream_t stream);
 
+/* INT8 GEMM a [M, K] x weight [N, K]^T with int8_linear's epilogue: acc * (a_scale * w_scale[n]) + bias[n] (two
+ * roundings), ReLU, BF16, GELU if gelu, then + residual [M, res_channels] (row stride res_row_stride) in FP32 -> BF16.
+ * a_scale_rows [M] (per-row dynamic activation scales) replaces *a_scale when non-NULL. out BF16 [M, N], or INT8 with
+ * out_scale. Replaces ops.int8_linear (flashim/ops/gemm.py:78-101) and int8_linear_quantize (:104-116). */
+int fim_int8_linear(const int8_t* a, int64_t M, int64_t K, const int8_t* weight, int64_t N, const float* a_scale,
+                    const float* a_scale_rows, const float* w_scale, const void* bias, int bias_dtype, int relu, int gelu,
+                    const void* residual, int res_dtype, int64_t res_channels, int64_t res_row_stride,
+                    const float* out_scale, void* out, hipStream_t stream);
+
+/* Block-scaled MXFP8 GEMM: a [M, K] E4M3 with per-(row, 32) E8M0 scales in cuBLAS' 128x4 swizzled layout, weight
+ * [N, K] E4M3 with int8 exponents [N, K/32] -> BF16 [M, N] (+ bias). Replaces ops.mxfp8_scaled_mm
+ * (flashim/ops/gemm.py:40-52; the caller passes b_t^T and unswizzled b exponents). */
+int fim_mxfp8_scaled_mm(const uint8_t* a, int64_t M, int64_t K, const uint8_t* a_scale_swizzled,
+                        const uint8_t* weight, int64_t N, const int8_t* weight_exponent, const void* bias,
+                        int bias_dtype, void* out, hipStream_t stream);
+
+/* im2col of a 1-byte NHWC tensor: out [B*Ho*Wo, kh*kw*C] in (ky, kx, c) order with zero padding. Replaces
+ * ops.im2col_gather (flashim/ops/conv.py:144-168). */
+int fim_im2col_gather(const uint8_t* x, int64_t B, int64_t H, int64_t W, int64_t C, int kh, int kw, int sh, int sw,
+                      int ph, int pw, int dh, int dw, uint8_t* out, hipStream_t stream);
+
 /* ---- depthwise 5x5 producers -------------------------------------------------------------------------------- */
 
 /* Depthwise 5x5, pad 2: x BF16 NHWC [B, H, W, C] (channels-last [B, C, H, W]), weight BF16 [25, C] (ky, kx major),

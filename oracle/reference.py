@@ -327,3 +327,21 @@ def depthwise5x5_gelu(value: Tensor, weight: Tensor, bias: Tensor, *, scale: Ten
     if exponent is not None:
         return quantize_static(rows, exponent)
     return rows.contiguous()
+
+
+def depthwise5x5_relu_pointwise_mxfp8(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
+                                      pw_scale_swizzled: Tensor, pw_scale_u8: Tensor, pw_bias: Tensor) -> Tensor:
+    """ops/conv.py:93-107: the dynamic MXFP8 producer then mxfp8_scaled_mm; a [B, C, H, W] view of NHWC BF16."""
+    batch, channels, height, width = value.shape
+    quantized, scale = depthwise5x5_relu_mxfp8(value, dw_weight, dw_bias)
+    out = mxfp8_scaled_mm(quantized, pw_weight.t(), scale, pw_scale_swizzled, pw_bias)
+    return out.reshape(batch, height, width, channels).permute(0, 3, 1, 2)
+
+
+def depthwise5x5_relu_pointwise_int8(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
+                                     pw_wscale: Tensor, pw_bias: Tensor, scale: Tensor) -> Tensor:
+    """ops/conv.py:119-132: the static INT8 producer then int8_linear; a [B, C, H, W] view of NHWC BF16."""
+    batch, channels, height, width = value.shape
+    quantized = depthwise5x5_relu_int8(value, dw_weight, dw_bias, scale)
+    out = int8_linear(quantized, pw_weight, scale, pw_wscale, pw_bias)
+    return out.reshape(batch, height, width, channels).permute(0, 3, 1, 2)
