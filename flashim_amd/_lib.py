@@ -41,6 +41,8 @@ SIGNATURES: dict[str, list] = {
         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
         _vp, _i32, _i64, _vp, _vp, _vp, _vp,
     ],
+    "fim_int8_conv2d_maxpool": [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i32] + [_i32] * 9
+    + [_vp, _vp, _vp, _vp],
     "fim_int8_linear": [
         _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _i64, _i64, _vp, _vp, _vp,
     ],

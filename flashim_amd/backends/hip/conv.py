@@ -76,6 +76,32 @@ def int8_conv2d(
     return out
 
 
+def int8_conv2d_maxpool(
+    x: Tensor, weight: Tensor, a_scale: Tensor, w_scale: Tensor, bias: Tensor | None,
+    kh: int, kw: int, sh: int, sw: int, ph: int, pw: int, dh: int, dw: int, *, relu: bool = False, out_scale: Tensor,
+) -> tuple[Tensor, Tensor]:
+    """``(out, pooled)``: the BF16 ``[B, Ho, Wo, Cout]`` conv output and the INT8 ``[B, Ho/2, Wo/2, Cout]`` 2x2 max pool
+    of it quantized with ``out_scale`` (``ops/conv.py:209-222``), the pool from the conv's epilogue."""
+    b, h, w, cin = x.shape
+    cout = weight.shape[0]
+    ho, wo = conv_output_size(h, w, kh, kw, sh, sw, ph, pw, dh, dw)
+    x = x.contiguous()
+    weight = weight.contiguous()
+    a_scale = a_scale.to(device=x.device, dtype=torch.float32).reshape(1).contiguous()
+    w_scale = w_scale.to(device=x.device, dtype=torch.float32).contiguous()
+    bias, bias_code = _bias_args(bias, x.device)
+    out_scale = out_scale.to(device=x.device, dtype=torch.float32).reshape(1).contiguous()
+    out = torch.empty(b, ho, wo, cout, device=x.device, dtype=torch.bfloat16)
+    pooled = torch.empty(b, ho // 2, wo // 2, cout, device=x.device, dtype=torch.int8)
+    _lib.call(
+        "fim_int8_conv2d_maxpool", x.data_ptr(), b, h, w, cin, weight.data_ptr(), cout, a_scale.data_ptr(),
+        w_scale.data_ptr(), _lib.ptr(bias), bias_code, kh, kw, sh, sw, ph, pw, dh, dw, int(relu), out_scale.data_ptr(),
+        out.data_ptr(), pooled.data_ptr(), _lib.stream_of(x),
+        what=f"int8_conv2d_maxpool {tuple(x.shape)} -> {cout} k{kh}x{kw}",
+    )
+    return out, pooled
+
+
 def mxfp8_conv2d(
     x: Tensor, channel_exponent: Tensor, weight: Tensor, weight_exponent: Tensor, bias: Tensor | None,
     kh: int, kw: int, sh: int, sw: int, ph: int, pw: int, dh: int, dw: int, *, relu: bool = False,
@@ -174,6 +200,12 @@ def eligible_int8_conv2d(x, weight, a_scale, w_scale, bias, kh, kw, sh, sw, ph, 
         and a_scale.numel() == 1 and w_scale.numel() == weight.shape[0]
         and (bias is None or bias.numel() == weight.shape[0])
     )
+
+
+def eligible_int8_conv2d_maxpool(x, weight, a_scale, w_scale, bias, kh, kw, sh, sw, ph, pw, dh, dw, *, relu=False,
+                                  out_scale=None) -> bool:
+    return out_scale is not None and out_scale.numel() == 1 and eligible_int8_conv2d(
+        x, weight, a_scale, w_scale, bias, kh, kw, sh, sw, ph, pw, dh, dw)
 
 
 def eligible_mxfp8_conv2d(x, channel_exponent, weight, weight_exponent, bias, kh, kw, sh, sw, ph, pw, dh, dw,

@@ -51,6 +51,7 @@ struct ConvArgs {
   const float* out_scale;  // OUT_INT8
   const int8_t* out_expo;  // OUT_E4M3: [Cout / 32]
   void* out;               // [B, Ho, Wo, Cout]
+  int8_t* pool_out;        // POOL: [B, Ho/2, Wo/2, Cout] int8, the 2x2 max pool of out quantized with out_scale
   int out_mode, relu_pre, relu_post, gelu;  // ReLU before the BF16 rounding / after the residual add
   int B, H, W, Cin, Ho, Wo, Cout;
   int kh, kw, sh, sw, ph, pw, dh, dw;
@@ -100,7 +101,28 @@ __device__ __forceinline__ uint4 load_seg(const uint8_t* p, bool row_ok, int cva
   return v;
 }
 
-template <int KIND, int BN, int LW, int OUT, int XS>
+// GEMM row m -> output pixel index (img * Ho + oh) * Wo + ow. Plain order is the identity; the pool order (POOL, Ho and
+// Wo even) puts the 4 pixels of each 2x2 pool window on 4 consecutive rows, windows in (img, oh / 2, ow / 2) order:
+// m = 4 * window + 2 * dy + dx.
+template <int POOL>
+__device__ __forceinline__ int pixel_of_row(const ConvArgs& a, int m, int& img, int& oh, int& ow) {
+  if (POOL) {
+    const int wo2 = a.Wo >> 1, ho2 = a.Ho >> 1;
+    const int win = m >> 2;
+    const int q = win / wo2;
+    ow = 2 * (win - q * wo2) + (m & 1);
+    img = q / ho2;
+    oh = 2 * (q - img * ho2) + ((m >> 1) & 1);
+    return (img * a.Ho + oh) * a.Wo + ow;
+  }
+  ow = m % a.Wo;
+  const int q = m / a.Wo;
+  img = q / a.Ho;
+  oh = q - img * a.Ho;
+  return m;
+}
+
+template <int KIND, int BN, int LW, int OUT, int XS, int POOL>
 __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
   constexpr int SXN = XS ? 4 : 1;        // activation scale registers per set: one per 16-pixel block with row scales
   constexpr int NB = BN / 32;            // 16-channel blocks per wavefront (BN/2 channels)
@@ -151,11 +173,9 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
   for (int j = 0; j < A_PASSES; ++j) {
     const int m = m0 + rsub + 32 * j;
     const bool ok = m < a.M;
-    const int mm = ok ? m : 0;
-    const int ow = mm % a.Wo;
-    const int q = mm / a.Wo;
-    const int img = q / a.Ho;
-    const int ih = (q % a.Ho) * a.sh - a.ph, iw = ow * a.sw - a.pw;
+    int img, oh, ow;
+    pixel_of_row<POOL>(a, ok ? m : 0, img, oh, ow);
+    const int ih = oh * a.sh - a.ph, iw = ow * a.sw - a.pw;
     a_h[j] = ok ? ih : -(1 << 28);  // an invalid row never passes the bounds test
     a_w[j] = iw;
     a_ptr[j] = a.x + ((int64_t)(img * a.H + ih) * a.W + iw) * a.Cin + seg * 16;
@@ -360,8 +380,8 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
   // ----- epilogue: straight from the accumulators. D[n][m] with lane = pixel (lane & 15) of a 16-pixel block and
   // 4 consecutive channels 4 (lane >> 4) + v of a 16-channel block: 4 channels of one pixel per store. Flags are
   // uniform (scalar branches); the output format is a template parameter.
-  const float out_scale = OUT == OUT_INT8 ? *a.out_scale : 1.0f;
-  const float out_inv = OUT == OUT_INT8 ? __fdiv_rn(1.0f, out_scale) : 1.0f;
+  const float out_scale = (OUT == OUT_INT8 || POOL) ? *a.out_scale : 1.0f;
+  const float out_inv = (OUT == OUT_INT8 || POOL) ? __fdiv_rn(1.0f, out_scale) : 1.0f;
   const bool has_bias = a.bias != nullptr;
   const bool res = a.residual != nullptr;
   const bool relu_pre = a.relu_pre != 0;
@@ -369,18 +389,16 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
   const bool res_vec = res && a.res_dtype == FIM_BF16 && a.rs_c == 1 && (((uintptr_t)a.residual) & 7) == 0 &&
                        (a.rs_w % 4) == 0 && (a.rs_h % 4) == 0 && (a.rs_b % 4) == 0;
   const bool out_vec = (a.Cout % 4) == 0;
-  int pm[MB];
+  int pm[MB], px[MB];
   int64_t roff[MB];
 #pragma unroll
   for (int j = 0; j < MB; ++j) {
     const int m = m0 + wm * 64 + j * 16 + (lane & 15);
     pm[j] = m;
     roff[j] = 0;
-    if (res && m < a.M) {
-      const int ow = m % a.Wo;
-      const int q = m / a.Wo;
-      roff[j] = (int64_t)(q / a.Ho) * a.rs_b + (int64_t)(q % a.Ho) * a.rs_h + (int64_t)ow * a.rs_w;
-    }
+    int img, oh, ow;
+    px[j] = pixel_of_row<POOL>(a, m < a.M ? m : 0, img, oh, ow);
+    if (res) roff[j] = (int64_t)img * a.rs_b + (int64_t)oh * a.rs_h + (int64_t)ow * a.rs_w;
   }
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
@@ -457,7 +475,31 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
           }
         }
       }
-      const int64_t o = (int64_t)m * a.Cout + nbase;
+      const int64_t o = (int64_t)px[j] * a.Cout + nbase;
+      if (POOL) {
+        // the window's 4 pixels sit on lanes 4k .. 4k + 3 of this 16-lane group (rows m = 4 * window + 0..3), all
+        // valid or all past M together: max across them, quantize (monotonic, so equal to quantizing the max of the
+        // quantized values), one 4-channel store per window
+        float p[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          p[v] = fmaxf(y[v], __shfl_xor(y[v], 1));
+          p[v] = fmaxf(p[v], __shfl_xor(p[v], 2));
+        }
+        if ((lane & 3) == 0) {
+          uint32_t pk = 0;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) pk |= (uint32_t)(uint8_t)quantize_int8_fast(p[v], out_scale, out_inv) << (8 * v);
+          uint8_t* pdst = reinterpret_cast<uint8_t*>(a.pool_out) + (int64_t)(m >> 2) * a.Cout + nbase;
+          if (out_vec && full) {
+            *reinterpret_cast<uint32_t*>(pdst) = pk;
+          } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              if (nbase + v < a.Cout) pdst[v] = (uint8_t)(pk >> (8 * v));
+          }
+        }
+      }
 #ifdef FIM_EPI_NOSTORE
       if (y[0] + y[1] + y[2] + y[3] == 12345.0f) static_cast<uint16_t*>(a.out)[o] = 1;
       continue;
@@ -497,12 +539,12 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
   FIM_STAMP(3);
 }
 
-template <int KIND, int BN, int OUT, int XS>
+template <int KIND, int BN, int OUT, int XS, int POOL = 0>
 static void launch_lw(const ConvArgs& a, int lw, dim3 grid, hipStream_t stream) {
   if (lw == 16)
-    conv_igemm_kernel<KIND, BN, 16, OUT, XS><<<grid, dim3(256), 0, stream>>>(a);
+    conv_igemm_kernel<KIND, BN, 16, OUT, XS, POOL><<<grid, dim3(256), 0, stream>>>(a);
   else
-    conv_igemm_kernel<KIND, BN, 1, OUT, XS><<<grid, dim3(256), 0, stream>>>(a);
+    conv_igemm_kernel<KIND, BN, 1, OUT, XS, POOL><<<grid, dim3(256), 0, stream>>>(a);
 }
 
 template <int KIND, int BN, int XS>
@@ -516,6 +558,12 @@ static void launch_bn(const ConvArgs& a, int lw, dim3 grid, hipStream_t stream) 
 
 template <int KIND, int BN>
 static void launch_xs(const ConvArgs& a, int lw, dim3 grid, hipStream_t stream) {
+  if constexpr (KIND == KIND_INT8) {
+    if (a.pool_out != nullptr) {
+      launch_lw<KIND, BN, OUT_BF16, 0, 1>(a, lw, grid, stream);
+      return;
+    }
+  }
   if constexpr (KIND == KIND_MX) {
     if (a.x_swz != nullptr) {
       launch_bn<KIND, 64, 1>(a, lw, grid, stream);  // row scales take 8 more VGPRs: the 64-channel tile keeps them
@@ -536,6 +584,10 @@ static int launch_conv(ConvArgs a, hipStream_t stream) {
   const int64_t M = (int64_t)a.B * a.Ho * a.Wo;
   if (M == 0) return FIM_OK;
   if (M >= (1LL << 31) - 256) return FIM_ERR_UNSUPPORTED;
+  if (a.pool_out != nullptr &&
+      (KIND != KIND_INT8 || (a.Ho | a.Wo) & 1 || a.out_mode != OUT_BF16 || a.out_scale == nullptr ||
+       a.residual != nullptr || a.a_scale_rows != nullptr))
+    return FIM_ERR_UNSUPPORTED;
   a.M = (int)M;
   a.kchunks = (a.Cin + KC - 1) / KC;
   const int bn = (a.Cout > 64 && a.x_swz == nullptr) ? 128 : 64;
@@ -581,6 +633,41 @@ static void fill_epilogue(ConvArgs& a, const void* bias, int bias_dtype, const v
 static bool dims_fit(int64_t B, int64_t H, int64_t W, int64_t Cin, int64_t Cout) {
   const int64_t lim = 2147483647LL;
   return B < lim && H < lim && W < lim && Cin < lim && Cout < lim && B * H * W < lim * 64;
+}
+
+// 2x2 / stride-2 max pool of BF16 [B, Ho, Wo, C] then INT8 quantize: one lane per 4 channels of a pooled pixel.
+__global__ __launch_bounds__(256) void pool2x2_quantize_kernel(const uint16_t* __restrict__ in, int64_t B, int64_t Ho,
+                                                               int64_t Wo, int64_t C, const float* scale_ptr,
+                                                               int8_t* __restrict__ out) {
+  const int64_t cq = (C + 3) >> 2;
+  const int64_t ho2 = Ho >> 1, wo2 = Wo >> 1;
+  const int64_t total = B * ho2 * wo2 * cq;
+  const float scale = *scale_ptr;
+  const float inv = __fdiv_rn(1.0f, scale);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t c0 = (i % cq) * 4;
+    const int64_t p = i / cq;
+    const int64_t x2 = p % wo2, q = p / wo2;
+    const int64_t y2 = q % ho2, img = q / ho2;
+    const uint16_t* base = in + ((img * Ho + 2 * y2) * Wo + 2 * x2) * C;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      if (c0 + v >= C) break;
+      const uint16_t* s = base + c0 + v;
+      const float m = fmaxf(fmaxf(bf16_to_f32(s[0]), bf16_to_f32(s[C])),
+                            fmaxf(bf16_to_f32(s[Wo * C]), bf16_to_f32(s[Wo * C + C])));
+      out[p * C + c0 + v] = quantize_int8_fast(m, scale, inv);
+    }
+  }
+}
+
+static int launch_pool2x2_quantize(const uint16_t* in, int64_t B, int64_t Ho, int64_t Wo, int64_t C,
+                                   const float* scale, int8_t* out, hipStream_t stream) {
+  const int64_t total = B * (Ho / 2) * (Wo / 2) * ((C + 3) / 4);
+  if (total == 0) return FIM_OK;
+  const int64_t blocks = std::min<int64_t>(cdiv(total, 256), 65536);
+  pool2x2_quantize_kernel<<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(in, B, Ho, Wo, C, scale, out);
+  return launch_status();
 }
 
 }  // namespace fim
@@ -630,6 +717,39 @@ int fim_mxfp8_conv2d(const uint8_t* x, int64_t B, int64_t H, int64_t W, int64_t 
   a.out_expo = out_exponent;
   a.out_mode = out_exponent != nullptr ? OUT_E4M3 : OUT_BF16;
   return launch_conv<KIND_MX>(a, stream);
+}
+
+// int8_conv2d then MaxPool2d(2) quantized for the next conv (ops/conv.py:209-222): out BF16 [B, Ho, Wo, Cout] as
+// fim_int8_conv2d writes it, pooled int8 [B, Ho/2, Wo/2, Cout] = quantize_int8(max_pool2d(out, 2), out_scale). Even
+// Ho and Wo: from the conv's epilogue (pool-ordered rows); odd: a separate pool pass over out (a trailing odd row /
+// column dropped, as F.max_pool2d does).
+int fim_int8_conv2d_maxpool(const int8_t* x, int64_t B, int64_t H, int64_t W, int64_t Cin, const int8_t* weight,
+                            int64_t Cout, const float* a_scale, const float* w_scale, const void* bias,
+                            int bias_dtype, int kh, int kw, int sh, int sw, int ph, int pw, int dh, int dw, int relu,
+                            const float* out_scale, void* out, int8_t* pooled, hipStream_t stream) {
+  if (x == nullptr || weight == nullptr || a_scale == nullptr || w_scale == nullptr || out == nullptr ||
+      out_scale == nullptr || pooled == nullptr)
+    return FIM_ERR_INVALID;
+  if (!dims_fit(B, H, W, Cin, Cout)) return FIM_ERR_UNSUPPORTED;
+  if (kh <= 0 || kw <= 0 || sh <= 0 || sw <= 0 || dh <= 0 || dw <= 0 || ph < 0 || pw < 0) return FIM_ERR_INVALID;
+  const int64_t Ho = (H + 2 * ph - (int64_t)dh * (kh - 1) - 1) / sh + 1;
+  const int64_t Wo = (W + 2 * pw - (int64_t)dw * (kw - 1) - 1) / sw + 1;
+  ConvArgs a = {};
+  a.x = reinterpret_cast<const uint8_t*>(x);
+  a.w = reinterpret_cast<const uint8_t*>(weight);
+  a.a_scale = a_scale;
+  a.w_scale = w_scale;
+  fill_geometry(a, B, H, W, Cin, Cout, kh, kw, sh, sw, ph, pw, dh, dw);
+  fill_epilogue(a, bias, bias_dtype, nullptr, 0, 0, nullptr, relu, 0, out);
+  a.out_scale = out_scale;
+  a.out_mode = OUT_BF16;
+  if (Ho > 0 && Wo > 0 && Ho % 2 == 0 && Wo % 2 == 0) {
+    a.pool_out = pooled;
+    return launch_conv<KIND_INT8>(a, stream);
+  }
+  const int rc = launch_conv<KIND_INT8>(a, stream);
+  if (rc != FIM_OK) return rc;
+  return launch_pool2x2_quantize(static_cast<const uint16_t*>(out), B, Ho, Wo, Cout, out_scale, pooled, stream);
 }
 
 // INT8 GEMM [M, K] x [N, K]^T with int8_linear's epilogue (ops/gemm.py:78-98): a 1x1 conv over a 1 x M "image".

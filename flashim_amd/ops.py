@@ -27,6 +27,7 @@ depthwise5x5_relu_int8 = Op("depthwise5x5_relu_int8")
 depthwise5x5_relu_pointwise_mxfp8 = Op("depthwise5x5_relu_pointwise_mxfp8", composite=True)
 depthwise5x5_relu_pointwise_int8 = Op("depthwise5x5_relu_pointwise_int8", composite=True)
 im2col_gather = Op("im2col_gather")
+int8_conv2d_maxpool = Op("int8_conv2d_maxpool", composite=True)
 int8_linear = Op("int8_linear")
 mxfp8_linear = Op("mxfp8_linear", weights=1)
 mxfp8_scaled_mm = Op("mxfp8_scaled_mm")
@@ -51,6 +52,8 @@ IMPLS = (
     ("depthwise5x5_relu_pointwise_int8", _conv.depthwise5x5_relu_pointwise_int8, (Feature.HIP, Feature.MFMA_I8),
      _conv.eligible_pointwise_int8),
     ("im2col_gather", _conv.im2col_gather, (Feature.HIP,), _conv.eligible_im2col),
+    ("int8_conv2d_maxpool", _conv.int8_conv2d_maxpool, (Feature.HIP, Feature.MFMA_I8),
+     _conv.eligible_int8_conv2d_maxpool),
     ("int8_linear", _gemm.int8_linear, (Feature.HIP, Feature.MFMA_I8), _gemm.eligible_int8_linear),
     ("mxfp8_linear", _gemm.mxfp8_linear, (Feature.HIP, Feature.MFMA_F8F6F4_SCALED), _gemm.eligible_mxfp8_linear),
     ("mxfp8_scaled_mm", _gemm.mxfp8_scaled_mm, (Feature.HIP, Feature.MFMA_F8F6F4_SCALED),

@@ -66,6 +66,7 @@ def impls(upstream_tensor_module) -> dict[str, tuple[Callable, Callable]]:
                                               _conv.eligible_pointwise_mxfp8),
         "depthwise5x5_relu_pointwise_int8": (_conv.depthwise5x5_relu_pointwise_int8, _conv.eligible_pointwise_int8),
         "im2col_gather": (_conv.im2col_gather, _conv.eligible_im2col),
+        "int8_conv2d_maxpool": (_conv.int8_conv2d_maxpool, _conv.eligible_int8_conv2d_maxpool),
         "int8_linear": (_gemm.int8_linear, _gemm.eligible_int8_linear),
         "mxfp8_scaled_mm": (_gemm.mxfp8_scaled_mm, _gemm.eligible_mxfp8_scaled_mm),
     }

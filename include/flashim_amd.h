@@ -91,6 +91,15 @@ int fim_mxfp8_conv2d(const uint8_t* x, int64_t B, int64_t H, int64_t W, int64_t 
                      const void* residual, int res_dtype, int64_t res_channels, const int64_t* res_strides,
                      const int8_t* out_exponent, void* out, hipStream_t stream);
 
+/* int8_conv2d (no residual) followed by MaxPool2d(2) and the next conv's static INT8 quantize: out BF16 [B, Ho, Wo,
+ * Cout] exactly as fim_int8_conv2d writes it, pooled int8 [B, Ho/2, Wo/2, Cout] = quantize(max_pool2d(out, 2),
+ * out_scale) (a trailing odd row / column dropped). Even Ho, Wo: pooled in the conv's epilogue; odd: one extra pass.
+ * Replaces ops.int8_conv2d_maxpool (flashim/ops/conv.py:209-222). */
+int fim_int8_conv2d_maxpool(const int8_t* x, int64_t B, int64_t H, int64_t W, int64_t Cin, const int8_t* weight,
+                            int64_t Cout, const float* a_scale, const float* w_scale, const void* bias,
+                            int bias_dtype, int kh, int kw, int sh, int sw, int ph, int pw, int dh, int dw, int relu,
+                            const float* out_scale, void* out, int8_t* pooled, hipStream_t stream);
+
 /* INT8 GEMM a [M, K] x weight [N, K]^T with int8_linear's epilogue: acc * (a_scale * w_scale[n]) + bias[n] (two
  * roundings), ReLU, BF16, GELU if gelu, then + residual [M, res_channels] (row stride res_row_stride) in FP32 -> BF16.
  * a_scale_rows [M] (per-row dynamic activation scales) replaces *a_scale when non-NULL. out BF16 [M, N], or INT8 with

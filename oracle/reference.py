@@ -264,6 +264,14 @@ def int8_conv2d(x: Tensor, weight: Tensor, a_scale: Tensor, w_scale: Tensor, bia
     return out if out_scale is None else quantize_int8_static(out, out_scale)
 
 
+def int8_conv2d_maxpool(x: Tensor, weight: Tensor, a_scale: Tensor, w_scale: Tensor, bias: Tensor | None,
+                        kh, kw, sh, sw, ph, pw, dh, dw, *, relu: bool = False, out_scale: Tensor):
+    """ops/conv.py:209-219: (BF16 conv output, INT8 quantize of its 2x2 max pool)."""
+    out = int8_conv2d(x, weight, a_scale, w_scale, bias, kh, kw, sh, sw, ph, pw, dh, dw, relu=relu)
+    pooled = F.max_pool2d(out.permute(0, 3, 1, 2), 2).permute(0, 2, 3, 1)
+    return out, quantize_int8_static(pooled, out_scale)
+
+
 def int8_conv2d_accumulators(x: Tensor, weight: Tensor, kh, kw, sh, sw, ph, pw, dh, dw) -> Tensor:
     """The int32 accumulators ``[B, Ho, Wo, Cout]`` of int8_conv2d (im2col -> int64 matmul)."""
     b, h, w, _ = x.shape

@@ -206,3 +206,28 @@ def test_repeated_launches_identical():
     ifirst = ops.int8_conv2d.get("hip")(*iargs, *geo)
     for _ in range(10):
         assert torch.equal(ops.int8_conv2d.get("hip")(*iargs, *geo), ifirst)
+
+
+MAXPOOL = [
+    ((2, 16, 20), 64, 64, (3, 3, 1, 1, 1, 1, 1, 1)),   # even Ho, Wo: pooled in the epilogue
+    ((1, 34, 18), 48, 40, (3, 3, 1, 1, 1, 1, 1, 1)),   # Cout % 4 == 0 but not 64-aligned, Cin % 16 != 0
+    ((2, 17, 19), 32, 96, (3, 3, 1, 1, 1, 1, 1, 1)),   # odd Ho, Wo: separate pool pass
+    ((1, 40, 40), 16, 130, (3, 3, 2, 2, 1, 1, 1, 1)),  # stride 2, Cout > 128 and % 4 != 0
+    ((3, 6, 10), 128, 64, (1, 1, 1, 1, 0, 0, 1, 1)),   # 1x1
+]
+
+
+@pytest.mark.parametrize("shape,cin,cout,geo", MAXPOOL)
+@pytest.mark.parametrize("relu", [False, True])
+def test_int8_conv2d_maxpool_bit_exact(shape, cin, cout, geo, relu):
+    """ops/conv.py:209-222: the BF16 output equals int8_conv2d's and the pooled INT8 codes equal quantize_int8 of
+    F.max_pool2d of it, bit for bit."""
+    x, weight, a_scale, w_scale, bias = _int8_inputs(cin, cout, geo[0], geo[1], True, shape=shape)
+    out_scale = torch.tensor(0.05)
+    out, pooled = ops.int8_conv2d_maxpool.get("hip")(*_dev(x, weight, a_scale, w_scale, bias), *geo, relu=relu,
+                                                     out_scale=out_scale.to(DEV))
+    want_out, want_pooled = ref.int8_conv2d_maxpool(x, weight, a_scale, w_scale, bias, *geo, relu=relu,
+                                                    out_scale=out_scale)
+    assert out.shape == want_out.shape and pooled.shape == want_pooled.shape and pooled.dtype == torch.int8
+    assert torch.equal(out.cpu(), want_out)
+    assert torch.equal(pooled.cpu(), want_pooled)
