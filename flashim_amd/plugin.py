@@ -52,6 +52,28 @@ def _adapt_quantized(upstream_tensor_module):
     return quantize_mxfp8, quantize_int8
 
 
+def _as_local(activation, weight):
+    """FlashIM's ``QuantizedTensor`` / ``QuantizedWeight`` share this package's field layout: re-wrap without copying."""
+    from flashim_amd import quant
+
+    act = quant.QuantizedTensor(activation.values, activation.scale_exponent, tuple(activation.logical_shape))
+    wgt = quant.QuantizedWeight(weight.values, weight.scale_exponent, tuple(weight.logical_shape))
+    return act, wgt
+
+
+def _mxfp8_linear(activation, bias, weight):
+    act, wgt = _as_local(activation, weight)
+    return _gemm.mxfp8_linear(act, bias, wgt)
+
+
+def _eligible_mxfp8_linear(activation, bias, weight) -> bool:
+    try:
+        act, wgt = _as_local(activation, weight)
+    except (AttributeError, ValueError, TypeError):
+        return False
+    return _gemm.eligible_mxfp8_linear(act, bias, wgt)
+
+
 def impls(upstream_tensor_module) -> dict[str, tuple[Callable, Callable]]:
     """``{op name: (impl, when)}`` for the FlashIM ops this backend replaces."""
     quantize_mxfp8, quantize_int8 = _adapt_quantized(upstream_tensor_module)
@@ -69,6 +91,7 @@ def impls(upstream_tensor_module) -> dict[str, tuple[Callable, Callable]]:
         "int8_conv2d_maxpool": (_conv.int8_conv2d_maxpool, _conv.eligible_int8_conv2d_maxpool),
         "int8_linear": (_gemm.int8_linear, _gemm.eligible_int8_linear),
         "mxfp8_scaled_mm": (_gemm.mxfp8_scaled_mm, _gemm.eligible_mxfp8_scaled_mm),
+        "mxfp8_linear": (_mxfp8_linear, _eligible_mxfp8_linear),
     }
 
 
