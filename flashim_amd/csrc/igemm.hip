@@ -63,7 +63,10 @@ struct ConvArgs {
 #ifdef FIM_TIMING
 __device__ unsigned long long fim_timing[16384][4];
 #define FIM_STAMP(k) \
-  do { if (threadIdx.x == 0 && blockIdx.x < 16384) fim_timing[blockIdx.x][k] = wall_clock64(); } while (0)
+  do { if (threadIdx.x == 0 && blockIdx.x < 16384) fim_timing[blockIdx.x][k] = (wall_clock64() & 0xffffffffffffULL) | ((unsigned long long)__smid() << 48); } while (0)
+extern "C" int fim_debug_timing(void* dst) {
+  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(fim_timing), sizeof(fim_timing), 0, hipMemcpyDeviceToHost);
+}
 #else
 #define FIM_STAMP(k) do { } while (0)
 #endif
@@ -120,6 +123,175 @@ __device__ __forceinline__ int pixel_of_row(const ConvArgs& a, int m, int& img, 
   img = q / a.Ho;
   oh = q - img * a.Ho;
   return m;
+}
+
+// Epilogue of one wavefront's MB x NB blocks of 16 x 16 outputs, straight from the accumulators: D[n][m] with
+// lane = pixel (lane & 15) of a 16-pixel block and 4 consecutive channels 4 (lane >> 4) + v of a 16-channel block, so
+// each store writes 4 channels of one pixel. row0: the wave's first GEMM row; n_tile0: the tile's first channel; nl0:
+// the wave's first channel within the tile (index into the per-channel operands ep_* staged in LDS).
+template <int KIND, int OUT, int POOL, int MB, int NB>
+__device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc_i)[NB][MB], const v4f (&acc_f)[NB][MB],
+                                              int row0, int n_tile0, int nl0, const float* ep_scale,
+                                              const float* ep_bias, const float* ep_oinv) {
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4;
+  // flags are uniform (scalar branches); the output format is a template parameter
+  const float out_scale = (OUT == OUT_INT8 || POOL) ? *a.out_scale : 1.0f;
+  const float out_inv = (OUT == OUT_INT8 || POOL) ? __fdiv_rn(1.0f, out_scale) : 1.0f;
+  const bool has_bias = a.bias != nullptr;
+  const bool res = a.residual != nullptr;
+  const bool relu_pre = a.relu_pre != 0;
+  const bool relu_post = a.relu_post != 0;
+  const bool res_vec = res && a.res_dtype == FIM_BF16 && a.rs_c == 1 && (((uintptr_t)a.residual) & 7) == 0 &&
+                       (a.rs_w % 4) == 0 && (a.rs_h % 4) == 0 && (a.rs_b % 4) == 0;
+  const bool out_vec = (a.Cout % 4) == 0;
+  int pm[MB], px[MB];
+  int64_t roff[MB];
+#pragma unroll
+  for (int j = 0; j < MB; ++j) {
+    const int m = row0 + j * 16 + (lane & 15);
+    pm[j] = m;
+    roff[j] = 0;
+    int img, oh, ow;
+    px[j] = pixel_of_row<POOL>(a, m < a.M ? m : 0, img, oh, ow);
+    if (res) roff[j] = (int64_t)img * a.rs_b + (int64_t)oh * a.rs_h + (int64_t)ow * a.rs_w;
+  }
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int nl = nl0 + i * 16 + 4 * g;
+    const int nbase = n_tile0 + nl;
+    const float4 cs4 = *reinterpret_cast<const float4*>(&ep_scale[nl]);
+    const float4 cb4 = *reinterpret_cast<const float4*>(&ep_bias[nl]);
+    const float4 ci4 = *reinterpret_cast<const float4*>(&ep_oinv[nl]);
+    const float cs[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
+    const float cb[4] = {cb4.x, cb4.y, cb4.z, cb4.w};
+    const float ci[4] = {ci4.x, ci4.y, ci4.z, ci4.w};
+    const bool full = nbase + 4 <= a.Cout;
+    const bool any = nbase < a.Cout;
+    const bool res_full = res_vec && nbase + 4 <= a.res_channels;
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const int m = pm[j];
+      if (!any || m >= a.M) continue;
+      float y[4];
+      if (KIND == KIND_INT8 && a.a_scale_rows != nullptr) {
+        const float arow = a.a_scale_rows[m];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) y[v] = __fmul_rn((float)acc_i[i][j][v], __fmul_rn(arow, cs[v]));
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) y[v] = KIND == KIND_INT8 ? __fmul_rn((float)acc_i[i][j][v], cs[v]) : acc_f[i][j][v];
+      }
+      if (has_bias) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) y[v] = __fadd_rn(y[v], cb[v]);
+      }
+      if (relu_pre) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) y[v] = fmaxf(y[v], 0.0f);
+      }
+      round_bf16x2(y[0], y[1]);
+      round_bf16x2(y[2], y[3]);
+      if (a.gelu) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) y[v] = gelu_erf(y[v]);
+        round_bf16x2(y[0], y[1]);
+        round_bf16x2(y[2], y[3]);
+      }
+      if (res) {
+        float rv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (res_full) {
+          const uint2 pk = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.residual) + roff[j] + nbase);
+          rv[0] = u2f(pk.x << 16);
+          rv[1] = u2f(pk.x & 0xffff0000u);
+          rv[2] = u2f(pk.y << 16);
+          rv[3] = u2f(pk.y & 0xffff0000u);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) y[v] = __fadd_rn(y[v], rv[v]);
+          if (relu_post) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) y[v] = fmaxf(y[v], 0.0f);
+          }
+          round_bf16x2(y[0], y[1]);
+          round_bf16x2(y[2], y[3]);
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int n = nbase + v;
+            if (n < a.res_channels) {
+              const int64_t off = roff[j] + (int64_t)n * a.rs_c;
+              const float r = a.res_dtype == FIM_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(a.residual)[off])
+                                                      : static_cast<const float*>(a.residual)[off];
+              float t = __fadd_rn(y[v], r);
+              if (relu_post) t = fmaxf(t, 0.0f);
+              y[v] = round_bf16(t);
+            } else if (relu_post) {
+              y[v] = fmaxf(y[v], 0.0f);
+            }
+          }
+        }
+      }
+      const int64_t o = (int64_t)px[j] * a.Cout + nbase;
+      if (POOL) {
+        // the window's 4 pixels sit on lanes 4k .. 4k + 3 of this 16-lane group (rows m = 4 * window + 0..3), all
+        // valid or all past M together: max across them, quantize (monotonic, so equal to quantizing the max of the
+        // quantized values), one 4-channel store per window
+        float p[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          p[v] = fmaxf(y[v], __shfl_xor(y[v], 1));
+          p[v] = fmaxf(p[v], __shfl_xor(p[v], 2));
+        }
+        if ((lane & 3) == 0) {
+          uint32_t pk = 0;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) pk |= (uint32_t)(uint8_t)quantize_int8_fast(p[v], out_scale, out_inv) << (8 * v);
+          uint8_t* pdst = reinterpret_cast<uint8_t*>(a.pool_out) + (int64_t)(m >> 2) * a.Cout + nbase;
+          if (out_vec && full) {
+            *reinterpret_cast<uint32_t*>(pdst) = pk;
+          } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              if (nbase + v < a.Cout) pdst[v] = (uint8_t)(pk >> (8 * v));
+          }
+        }
+      }
+#ifdef FIM_EPI_NOSTORE
+      if (y[0] + y[1] + y[2] + y[3] == 12345.0f) static_cast<uint16_t*>(a.out)[o] = 1;
+      continue;
+#endif
+      if (OUT == OUT_BF16) {
+        uint16_t* dst = static_cast<uint16_t*>(a.out) + o;
+        const uint32_t lo = pack_bf16x2(y[0], y[1]), hi = pack_bf16x2(y[2], y[3]);
+        if (out_vec && full) {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+        } else {
+          const uint16_t h[4] = {(uint16_t)lo, (uint16_t)(lo >> 16), (uint16_t)hi, (uint16_t)(hi >> 16)};
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (nbase + v < a.Cout) dst[v] = h[v];
+        }
+      } else {
+        uint32_t pk;
+        if (OUT == OUT_INT8) {
+          pk = 0;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) pk |= (uint32_t)(uint8_t)quantize_int8_fast(y[v], out_scale, out_inv) << (8 * v);
+        } else {
+          pk = pack_e4m3x4(mx_scale_clamp(y[0], ci[0]), mx_scale_clamp(y[1], ci[1]), mx_scale_clamp(y[2], ci[2]),
+                           mx_scale_clamp(y[3], ci[3]));
+        }
+        uint8_t* dst = static_cast<uint8_t*>(a.out) + o;
+        if (out_vec && full) {
+          *reinterpret_cast<uint32_t*>(dst) = pk;
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (nbase + v < a.Cout) dst[v] = (uint8_t)(pk >> (8 * v));
+        }
+      }
+    }
+  }
 }
 
 template <int KIND, int BN, int LW, int OUT, int XS, int POOL>
@@ -377,167 +549,10 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
   }
 
   FIM_STAMP(2);
-  // ----- epilogue: straight from the accumulators. D[n][m] with lane = pixel (lane & 15) of a 16-pixel block and
-  // 4 consecutive channels 4 (lane >> 4) + v of a 16-channel block: 4 channels of one pixel per store. Flags are
-  // uniform (scalar branches); the output format is a template parameter.
-  const float out_scale = (OUT == OUT_INT8 || POOL) ? *a.out_scale : 1.0f;
-  const float out_inv = (OUT == OUT_INT8 || POOL) ? __fdiv_rn(1.0f, out_scale) : 1.0f;
-  const bool has_bias = a.bias != nullptr;
-  const bool res = a.residual != nullptr;
-  const bool relu_pre = a.relu_pre != 0;
-  const bool relu_post = a.relu_post != 0;
-  const bool res_vec = res && a.res_dtype == FIM_BF16 && a.rs_c == 1 && (((uintptr_t)a.residual) & 7) == 0 &&
-                       (a.rs_w % 4) == 0 && (a.rs_h % 4) == 0 && (a.rs_b % 4) == 0;
-  const bool out_vec = (a.Cout % 4) == 0;
-  int pm[MB], px[MB];
-  int64_t roff[MB];
-#pragma unroll
-  for (int j = 0; j < MB; ++j) {
-    const int m = m0 + wm * 64 + j * 16 + (lane & 15);
-    pm[j] = m;
-    roff[j] = 0;
-    int img, oh, ow;
-    px[j] = pixel_of_row<POOL>(a, m < a.M ? m : 0, img, oh, ow);
-    if (res) roff[j] = (int64_t)img * a.rs_b + (int64_t)oh * a.rs_h + (int64_t)ow * a.rs_w;
-  }
-#pragma unroll
-  for (int i = 0; i < NB; ++i) {
-    const int nbase = n0 + wn * (BN / 2) + i * 16 + 4 * g;
-    const int nl = nbase - n0;
-    const float4 cs4 = *reinterpret_cast<const float4*>(&ep_scale[nl]);
-    const float4 cb4 = *reinterpret_cast<const float4*>(&ep_bias[nl]);
-    const float4 ci4 = *reinterpret_cast<const float4*>(&ep_oinv[nl]);
-    const float cs[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
-    const float cb[4] = {cb4.x, cb4.y, cb4.z, cb4.w};
-    const float ci[4] = {ci4.x, ci4.y, ci4.z, ci4.w};
-    const bool full = nbase + 4 <= a.Cout;
-    const bool any = nbase < a.Cout;
-    const bool res_full = res_vec && nbase + 4 <= a.res_channels;
-#pragma unroll
-    for (int j = 0; j < MB; ++j) {
-      const int m = pm[j];
-      if (!any || m >= a.M) continue;
-      float y[4];
-      if (KIND == KIND_INT8 && a.a_scale_rows != nullptr) {
-        const float arow = a.a_scale_rows[m];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) y[v] = __fmul_rn((float)acc_i[i][j][v], __fmul_rn(arow, cs[v]));
-      } else {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) y[v] = KIND == KIND_INT8 ? __fmul_rn((float)acc_i[i][j][v], cs[v]) : acc_f[i][j][v];
-      }
-      if (has_bias) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) y[v] = __fadd_rn(y[v], cb[v]);
-      }
-      if (relu_pre) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) y[v] = fmaxf(y[v], 0.0f);
-      }
-      round_bf16x2(y[0], y[1]);
-      round_bf16x2(y[2], y[3]);
-      if (a.gelu) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) y[v] = gelu_erf(y[v]);
-        round_bf16x2(y[0], y[1]);
-        round_bf16x2(y[2], y[3]);
-      }
-      if (res) {
-        float rv[4] = {0.f, 0.f, 0.f, 0.f};
-        if (res_full) {
-          const uint2 pk = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.residual) + roff[j] + nbase);
-          rv[0] = u2f(pk.x << 16);
-          rv[1] = u2f(pk.x & 0xffff0000u);
-          rv[2] = u2f(pk.y << 16);
-          rv[3] = u2f(pk.y & 0xffff0000u);
-#pragma unroll
-          for (int v = 0; v < 4; ++v) y[v] = __fadd_rn(y[v], rv[v]);
-          if (relu_post) {
-#pragma unroll
-            for (int v = 0; v < 4; ++v) y[v] = fmaxf(y[v], 0.0f);
-          }
-          round_bf16x2(y[0], y[1]);
-          round_bf16x2(y[2], y[3]);
-        } else {
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int n = nbase + v;
-            if (n < a.res_channels) {
-              const int64_t off = roff[j] + (int64_t)n * a.rs_c;
-              const float r = a.res_dtype == FIM_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(a.residual)[off])
-                                                      : static_cast<const float*>(a.residual)[off];
-              float t = __fadd_rn(y[v], r);
-              if (relu_post) t = fmaxf(t, 0.0f);
-              y[v] = round_bf16(t);
-            } else if (relu_post) {
-              y[v] = fmaxf(y[v], 0.0f);
-            }
-          }
-        }
-      }
-      const int64_t o = (int64_t)px[j] * a.Cout + nbase;
-      if (POOL) {
-        // the window's 4 pixels sit on lanes 4k .. 4k + 3 of this 16-lane group (rows m = 4 * window + 0..3), all
-        // valid or all past M together: max across them, quantize (monotonic, so equal to quantizing the max of the
-        // quantized values), one 4-channel store per window
-        float p[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          p[v] = fmaxf(y[v], __shfl_xor(y[v], 1));
-          p[v] = fmaxf(p[v], __shfl_xor(p[v], 2));
-        }
-        if ((lane & 3) == 0) {
-          uint32_t pk = 0;
-#pragma unroll
-          for (int v = 0; v < 4; ++v) pk |= (uint32_t)(uint8_t)quantize_int8_fast(p[v], out_scale, out_inv) << (8 * v);
-          uint8_t* pdst = reinterpret_cast<uint8_t*>(a.pool_out) + (int64_t)(m >> 2) * a.Cout + nbase;
-          if (out_vec && full) {
-            *reinterpret_cast<uint32_t*>(pdst) = pk;
-          } else {
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-              if (nbase + v < a.Cout) pdst[v] = (uint8_t)(pk >> (8 * v));
-          }
-        }
-      }
-#ifdef FIM_EPI_NOSTORE
-      if (y[0] + y[1] + y[2] + y[3] == 12345.0f) static_cast<uint16_t*>(a.out)[o] = 1;
-      continue;
-#endif
-      if (OUT == OUT_BF16) {
-        uint16_t* dst = static_cast<uint16_t*>(a.out) + o;
-        const uint32_t lo = pack_bf16x2(y[0], y[1]), hi = pack_bf16x2(y[2], y[3]);
-        if (out_vec && full) {
-          *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
-        } else {
-          const uint16_t h[4] = {(uint16_t)lo, (uint16_t)(lo >> 16), (uint16_t)hi, (uint16_t)(hi >> 16)};
-#pragma unroll
-          for (int v = 0; v < 4; ++v)
-            if (nbase + v < a.Cout) dst[v] = h[v];
-        }
-      } else {
-        uint32_t pk;
-        if (OUT == OUT_INT8) {
-          pk = 0;
-#pragma unroll
-          for (int v = 0; v < 4; ++v) pk |= (uint32_t)(uint8_t)quantize_int8_fast(y[v], out_scale, out_inv) << (8 * v);
-        } else {
-          pk = pack_e4m3x4(mx_scale_clamp(y[0], ci[0]), mx_scale_clamp(y[1], ci[1]), mx_scale_clamp(y[2], ci[2]),
-                           mx_scale_clamp(y[3], ci[3]));
-        }
-        uint8_t* dst = static_cast<uint8_t*>(a.out) + o;
-        if (out_vec && full) {
-          *reinterpret_cast<uint32_t*>(dst) = pk;
-        } else {
-#pragma unroll
-          for (int v = 0; v < 4; ++v)
-            if (nbase + v < a.Cout) dst[v] = (uint8_t)(pk >> (8 * v));
-        }
-      }
-    }
-  }
+  conv_epilogue<KIND, OUT, POOL, MB, NB>(a, acc_i, acc_f, m0 + wm * 64, n0, wn * (BN / 2), ep_scale, ep_bias, ep_oinv);
   FIM_STAMP(3);
 }
+
 
 template <int KIND, int BN, int OUT, int XS, int POOL = 0>
 static void launch_lw(const ConvArgs& a, int lw, dim3 grid, hipStream_t stream) {
@@ -590,15 +605,15 @@ static int launch_conv(ConvArgs a, hipStream_t stream) {
     return FIM_ERR_UNSUPPORTED;
   a.M = (int)M;
   a.kchunks = (a.Cin + KC - 1) / KC;
+  int lw = 1;
+  const uintptr_t both = (uintptr_t)a.x | (uintptr_t)a.w;
+  if (a.Cin % 16 == 0 && both % 16 == 0) lw = 16;
   const int bn = (a.Cout > 64 && a.x_swz == nullptr) ? 128 : 64;
   a.n_tiles = (a.Cout + bn - 1) / bn;
   const int64_t m_tiles = (a.M + BM - 1) / BM;
   const int64_t tiles = m_tiles * a.n_tiles;
   if (tiles > (1LL << 30)) return FIM_ERR_UNSUPPORTED;
   a.m_tiles = (int)m_tiles;
-  int lw = 1;
-  const uintptr_t both = (uintptr_t)a.x | (uintptr_t)a.w;
-  if (a.Cin % 16 == 0 && both % 16 == 0) lw = 16;
   dim3 grid((unsigned)(cdiv(tiles, 8) * 8));  // a multiple of the 8 XCDs: the kernel maps pids to tiles per XCD
   if (bn == 128)
     launch_xs<KIND, 128>(a, lw, grid, stream);
