@@ -48,6 +48,8 @@ SIGNATURES: dict[str, list] = {
     ],
     "fim_mxfp8_scaled_mm": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i32, _vp, _vp],
     "fim_im2col_gather": [_vp, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp],
+    "fim_refiner_mlp": [_i32, _i32, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _vp,
+                        _vp],
     "fim_depthwise5x5": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp],
     "fim_test_e4m3": [_vp, _i64, _vp, _vp],
     "fim_test_mx_exponent": [_vp, _i64, _vp, _vp],

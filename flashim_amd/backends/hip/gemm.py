@@ -3,6 +3,8 @@
 * ``int8_linear``     (``flashim/ops/gemm.py:78-101``)  -> ``fim_int8_linear``
 * ``mxfp8_linear``    (``flashim/ops/gemm.py:58-72``)   -> ``fim_mxfp8_conv2d`` on a 1 x rows image
 * ``mxfp8_scaled_mm`` (``flashim/ops/gemm.py:40-52``)   -> ``fim_mxfp8_scaled_mm`` (per-row swizzled scales)
+* ``mxfp8_gelu_mlp``  (``flashim/ops/gemm.py:146-157``) -> ``fim_refiner_mlp`` (the fused MLP, hidden kept in LDS;
+  64 -> 256 -> 64 channels), and the refiner block's pointwise pair on the same kernel (:func:`refiner_mlp`)
 """
 
 from __future__ import annotations
@@ -85,6 +87,69 @@ def mxfp8_scaled_mm(a: Tensor, b_t: Tensor, a_scale: Tensor, b_scale: Tensor, bi
         _lib.stream_of(a), what=f"mxfp8_scaled_mm {m}x{k} -> {n}",
     )
     return out
+
+
+MLP_CHANNELS, MLP_HIDDEN = 64, 256  # the fused MLP kernel's shape
+
+
+def mxfp8_gelu_mlp(x: quant.QuantizedTensor, w1: quant.QuantizedWeight, b1: Tensor, hidden_exponent: Tensor,
+                   w2: quant.QuantizedWeight) -> Tensor:
+    """``quantize_static(GELU(x W1^T [BF16] + b1) [BF16], hidden_exponent) W2^T`` -> BF16 ``[rows, N2]``
+    (``flashim/ops/gemm.py:146-157``) in one launch."""
+    a = x.matrix().contiguous()
+    rows = a.shape[0]
+    b1 = b1.to(device=a.device).contiguous()
+    b1_code = 1 if b1.dtype == torch.bfloat16 else 0
+    if b1_code == 0:
+        b1 = b1.float()
+    out = torch.empty(rows, w2.values.shape[0], device=a.device, dtype=torch.bfloat16)
+    _lib.call(
+        "fim_refiner_mlp", 1, 1, a.data_ptr(), rows, MLP_CHANNELS, MLP_HIDDEN, x.scale_exponent.contiguous().data_ptr(),
+        w1.values.contiguous().data_ptr(), w1.scale_exponent.contiguous().data_ptr(), b1.data_ptr(), b1_code,
+        hidden_exponent.to(torch.int8).contiguous().data_ptr(), w2.values.contiguous().data_ptr(),
+        w2.scale_exponent.contiguous().data_ptr(), None, 0, None, out.data_ptr(), _lib.stream_of(a),
+        what=f"mxfp8_gelu_mlp {rows}x{MLP_CHANNELS}",
+    )
+    return out
+
+
+def eligible_mxfp8_gelu_mlp(x, w1, b1, hidden_exponent, w2) -> bool:
+    return (
+        isinstance(x, quant.QuantizedTensor) and is_gfx950(x.device) and x.channels == MLP_CHANNELS
+        and isinstance(w1, quant.QuantizedWeight) and isinstance(w2, quant.QuantizedWeight)
+        and tuple(w1.values.shape) == (MLP_HIDDEN, MLP_CHANNELS) and tuple(w2.values.shape) == (MLP_CHANNELS, MLP_HIDDEN)
+        and hidden_exponent.numel() == MLP_HIDDEN // 32 and b1.numel() == MLP_HIDDEN
+    )
+
+
+def refiner_mlp(x: Tensor, x_scale: Tensor, w1: Tensor, w1_scale: Tensor, b1: Tensor | None, hidden_scale: Tensor,
+                w2: Tensor, w2_scale: Tensor, b2: Tensor | None, residual: Tensor | None) -> Tensor:
+    """The refiner block's pointwise pair in one launch, bit for bit what the two 1x1 conv launches it replaces
+    compute: ``conv1x1(x; W1, b1, GELU, static quantize with hidden_scale)`` then ``conv1x1(.; W2, b2) + residual``.
+    INT8 (``x`` int8, FP32 scalar scales, FP32 per-channel weight scales) or MXFP8 (``x`` E4M3, int8 exponents).
+    ``x``: ``[..., 64]``; returns BF16 of the same leading shape."""
+    mx = x.dtype == torch.float8_e4m3fn
+    lead = x.shape[:-1]
+    a = x.reshape(-1, MLP_CHANNELS).contiguous()
+    rows = a.shape[0]
+
+    def scale(t: Tensor) -> Tensor:
+        return t.to(device=a.device, dtype=torch.int8 if mx else torch.float32).contiguous()
+
+    b1, b1_code = _bias(b1, a.device)
+    b2, b2_code = _bias(b2, a.device)
+    res = None
+    if residual is not None:
+        res = residual.reshape(-1, MLP_CHANNELS).to(torch.bfloat16).contiguous()
+    out = torch.empty(rows, MLP_CHANNELS, device=a.device, dtype=torch.bfloat16)
+    xs, w1s, hs, w2s = scale(x_scale), scale(w1_scale), scale(hidden_scale), scale(w2_scale)
+    _lib.call(
+        "fim_refiner_mlp", 1 if mx else 0, 0, a.view(torch.uint8).data_ptr(), rows, MLP_CHANNELS, MLP_HIDDEN,
+        xs.data_ptr(), w1.contiguous().view(torch.uint8).data_ptr(), w1s.data_ptr(), _lib.ptr(b1), b1_code,
+        hs.data_ptr(), w2.contiguous().view(torch.uint8).data_ptr(), w2s.data_ptr(), _lib.ptr(b2), b2_code,
+        _lib.ptr(res), out.data_ptr(), _lib.stream_of(a), what=f"refiner_mlp {rows}x{MLP_CHANNELS}",
+    )
+    return out.view(*lead, MLP_CHANNELS)
 
 
 # -- eligibility ----------------------------------------------------------------------------------------------------

@@ -9,6 +9,9 @@ Block (channels ``C``, hidden ``4C``), the depthwise-then-pointwise structure of
    with ``gelu=True`` and the chained quant-out epilogue, quant/methods/conv2d.py:102-125, 207-251);
 4. 1x1 contract 4C -> C, bias, + residual (the block input) -> BF16 (the residual epilogue, ops/conv.py:198-203).
 
+At C = 64, steps 3-4 run as one fused launch (``refiner_mlp``: the quantized hidden layer never leaves LDS), computing
+exactly what the two conv launches compute.
+
 Presets: ``"mxfp8"`` (E4M3, static per-32-channel exponents, per-(row, 32) weight exponents) and ``"int8"`` (per-tensor
 static activation scales, per-output-channel weights). Activations are NHWC BF16 ``[B, H, W, C]`` between blocks.
 Static activation scales come from one calibration pass over a sample input (what FlashIM's calibration tables hold).
@@ -22,6 +25,7 @@ import torch
 from torch import Tensor
 
 from flashim_amd import ops, quant
+from flashim_amd.backends.hip import gemm as _gemm
 
 BN_EPS = 1e-5
 
@@ -111,13 +115,21 @@ class RefinerBlock:
 
     def forward(self, x: Tensor) -> Tensor:
         b, h, w, c = x.shape
+        fused = c == _gemm.MLP_CHANNELS  # the pointwise pair in one launch (bit-identical to the two convs)
         if self.preset == "mxfp8":
             q1 = ops.depthwise5x5_gelu(x.permute(0, 3, 1, 2), self.dw_weight, self.dw_bias, exponent=self.in_scale)
+            if fused:
+                return _gemm.refiner_mlp(q1.view(b, h, w, c), self.in_scale, self.w1.values, self.w1.scale_exponent,
+                                         self.b1, self.hidden_scale, self.w2.values, self.w2.scale_exponent, self.b2,
+                                         x)
             q2 = ops.mxfp8_conv2d(q1.view(b, h, w, c), self.in_scale, self.w1.values, self.w1.scale_exponent, self.b1,
                                   1, 1, 1, 1, 0, 0, 1, 1, gelu=True, out_exponent=self.hidden_scale)
             return ops.mxfp8_conv2d(q2, self.hidden_scale, self.w2.values, self.w2.scale_exponent, self.b2,
                                     1, 1, 1, 1, 0, 0, 1, 1, residual=x)
         q1 = ops.depthwise5x5_gelu(x.permute(0, 3, 1, 2), self.dw_weight, self.dw_bias, scale=self.in_scale)
+        if fused:
+            return _gemm.refiner_mlp(q1.view(b, h, w, c), self.in_scale, self.w1_q, self.w1_s, self.b1,
+                                     self.hidden_scale, self.w2_q, self.w2_s, self.b2, x)
         q2 = ops.int8_conv2d(q1.view(b, h, w, c), self.w1_q, self.in_scale, self.w1_s, self.b1,
                              1, 1, 1, 1, 0, 0, 1, 1, gelu=True, out_scale=self.hidden_scale)
         return ops.int8_conv2d(q2, self.w2_q, self.hidden_scale, self.w2_s, self.b2, 1, 1, 1, 1, 0, 0, 1, 1,

@@ -31,6 +31,7 @@ int8_conv2d_maxpool = Op("int8_conv2d_maxpool", composite=True)
 int8_linear = Op("int8_linear")
 mxfp8_linear = Op("mxfp8_linear", weights=1)
 mxfp8_scaled_mm = Op("mxfp8_scaled_mm")
+mxfp8_gelu_mlp = Op("mxfp8_gelu_mlp")
 # this backend's refiner-block producer (folded BatchNorm + GELU)
 depthwise5x5_gelu = Op("depthwise5x5_gelu")
 
@@ -58,6 +59,7 @@ IMPLS = (
     ("mxfp8_linear", _gemm.mxfp8_linear, (Feature.HIP, Feature.MFMA_F8F6F4_SCALED), _gemm.eligible_mxfp8_linear),
     ("mxfp8_scaled_mm", _gemm.mxfp8_scaled_mm, (Feature.HIP, Feature.MFMA_F8F6F4_SCALED),
      _gemm.eligible_mxfp8_scaled_mm),
+    ("mxfp8_gelu_mlp", _gemm.mxfp8_gelu_mlp, (Feature.HIP, Feature.MFMA_F8F6F4_SCALED), _gemm.eligible_mxfp8_gelu_mlp),
 )
 
 for _name, _fn, _requires, _when in IMPLS:

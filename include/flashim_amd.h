@@ -116,6 +116,19 @@ int fim_mxfp8_scaled_mm(const uint8_t* a, int64_t M, int64_t K, const uint8_t* a
                         const uint8_t* weight, int64_t N, const int8_t* weight_exponent, const void* bias,
                         int bias_dtype, void* out, hipStream_t stream);
 
+/* Fused MLP, C = 64 -> H = 256 -> C = 64 rows of x [P, C] (hidden layer quantized into LDS, never written out).
+ * kind 0 INT8 (x_scale, h_scale FP32 scalars; w1_scale FP32 [H], w2_scale FP32 [C]), 1 MXFP8 (x_scale int8 [C/32],
+ * w1_scale int8 [H, C/32], h_scale int8 [H/32], w2_scale int8 [C, H/32]). w1 [H, C], w2 [C, H]; out BF16 [P, C].
+ * semantics 1 (MXFP8, b2 and residual null) replaces ops.mxfp8_gelu_mlp (flashim/ops/gemm.py:146-157):
+ *   bf16(quantize_static(bf16(gelu(bf16(x W1^T) + b1)), h) W2^T).
+ * semantics 0 is the conv-refiner block's pointwise pair, identical to fim_int8_conv2d / fim_mxfp8_conv2d 1x1 with
+ * (b1, GELU, quantized output h_scale) followed by 1x1 with (b2, + residual BF16 [P, C]): the two launches it
+ * replaces (flashim/ops/conv.py:174-206, 309-342; quant/methods/conv2d.py:102-125). 99 for any other C or H. */
+int fim_refiner_mlp(int kind, int semantics, const uint8_t* x, int64_t P, int64_t C, int64_t H, const void* x_scale,
+                    const uint8_t* w1, const void* w1_scale, const void* b1, int b1_dtype, const void* h_scale,
+                    const uint8_t* w2, const void* w2_scale, const void* b2, int b2_dtype, const uint16_t* residual,
+                    uint16_t* out, hipStream_t stream);
+
 /* im2col of a 1-byte NHWC tensor: out [B*Ho*Wo, kh*kw*C] in (ky, kx, c) order with zero padding. Replaces
  * ops.im2col_gather (flashim/ops/conv.py:144-168). */
 int fim_im2col_gather(const uint8_t* x, int64_t B, int64_t H, int64_t W, int64_t C, int kh, int kw, int sh, int sw,

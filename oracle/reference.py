@@ -208,6 +208,15 @@ def mxfp8_linear(values: Tensor, scale_exponent: Tensor, bias: Tensor | None, w_
     return out.to(torch.bfloat16)
 
 
+def mxfp8_gelu_mlp(values: Tensor, scale_exponent: Tensor, w1_values: Tensor, w1_exponent: Tensor, b1: Tensor,
+                   hidden_exponent: Tensor, w2_values: Tensor, w2_exponent: Tensor) -> Tensor:
+    """ops/gemm.py:146-157: hidden = mxfp8_linear(x, None, w1) (BF16); gelu(hidden.float() + b1.float()) -> BF16;
+    quantize_static(., hidden_exponent); mxfp8_linear(., None, w2) -> BF16."""
+    hidden = mxfp8_linear(values, scale_exponent, None, w1_values, w1_exponent)
+    activated = F.gelu(hidden.float() + b1.float()).to(torch.bfloat16)
+    return mxfp8_linear(quantize_static(activated, hidden_exponent), hidden_exponent, None, w2_values, w2_exponent)
+
+
 def mxfp8_scaled_mm(a: Tensor, b_t: Tensor, a_scale: Tensor, b_scale: Tensor, bias: Tensor | None = None) -> Tensor:
     """ops/gemm.py:40-49."""
     a_dense = dequantize_swizzled(a, a_scale)
