@@ -24,6 +24,13 @@ enum { MLP_BLOCK = 0, MLP_REFERENCE = 1 };
 
 constexpr int MLP_C = 64, MLP_H = 256, MLP_BM = 64;
 
+#ifdef FIM_TIMING
+__device__ unsigned long long fim_mlp_timing[1024][4];
+#define MLP_T(k) unsigned long long _t##k = wall_clock64()
+#else
+#define MLP_T(k) do { } while (0)
+#endif
+
 struct MlpArgs {
   const uint8_t* x;        // [P, C] int8 / E4M3
   const uint8_t* w1;       // [H, C]
@@ -113,14 +120,35 @@ __global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
     if (t < a.ntiles && px < a.P) return *reinterpret_cast<const uint4*>(a.x + (int64_t)px * MLP_C + ld_seg * 16);
     return make_uint4(0, 0, 0, 0);
   };
+  // the residual of a tile, prefetched with its input: lane (wave, r16, g) adds pixel 16 wave + r16, channels
+  // 16 i + 4 g .. + 3
+  auto load_res = [&](int t, uint2 (&r)[4]) {
+    const int px = t * MLP_BM + 16 * wave + r16;
+    const bool ok = a.residual != nullptr && t < a.ntiles && px < a.P;
+    const uint16_t* src = a.residual + (int64_t)(ok ? px : 0) * MLP_C + 4 * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint2 v = ok ? *reinterpret_cast<const uint2*>(src + 16 * i) : make_uint2(0, 0);
+      r[i] = v;
+    }
+  };
   uint4 cur = load_tile(blockIdx.x);
+  uint2 res_cur[4], res_nxt[4];
+  load_res(blockIdx.x, res_cur);
   __syncthreads();  // weights and tables staged
 
+#ifdef FIM_TIMING
+  unsigned long long ph[4] = {0, 0, 0, 0};
+  const unsigned long long t_begin = wall_clock64();
+#endif
   for (int t = blockIdx.x; t < a.ntiles; t += gridDim.x) {
+    MLP_T(0);
     const int px0 = t * MLP_BM;
     *reinterpret_cast<uint4*>(&xs[ld_dst]) = cur;
     __syncthreads();  // input tile staged; the previous tile's hidden reads are done
-    cur = load_tile(t + gridDim.x);  // prefetch
+    MLP_T(1);
+    cur = load_tile(t + gridDim.x);  // prefetch the next tile's input and residual
+    load_res(t + gridDim.x, res_nxt);
 
     // ---- expand: wave w computes hidden channels [64 w, 64 w + 64) x all 64 pixels ----------------------------
     // all 16 MFMAs first (their latency then hides behind each other), the VALU-heavy epilogues after
@@ -179,8 +207,10 @@ __global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
             round_bf16x2(y[0], y[1]);
             round_bf16x2(y[2], y[3]);
           }
+#ifndef FIM_EXP_NOGELU
 #pragma unroll
           for (int v = 0; v < 4; ++v) y[v] = gelu_erf(y[v]);
+#endif
           round_bf16x2(y[0], y[1]);
           round_bf16x2(y[2], y[3]);
           uint32_t q;
@@ -197,20 +227,16 @@ __global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
         }
       }
     }
+    MLP_T(2);
     __syncthreads();  // hidden tile complete
+    MLP_T(3);
 
     // ---- contract: wave w computes pixels [16 w, 16 w + 16) x all 64 channels ---------------------------------
     {
       const int prow = 16 * wave + r16;  // the hidden row this lane's B fragments come from
       const int px = px0 + prow;         // and the output pixel of this lane's results
       const bool pok = px < a.P;
-      uint2 res[4];
-      if (a.residual != nullptr) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          res[i] = pok ? *reinterpret_cast<const uint2*>(a.residual + (int64_t)px * MLP_C + 16 * i + 4 * g)
-                       : make_uint2(0, 0);
-      }
+      const uint2 (&res)[4] = res_cur;
       v4i acc_i[4] = {};
       v4f acc_f[4] = {};
       if (KIND == MLP_INT8) {
@@ -266,8 +292,25 @@ __global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
               make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
       }
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) res_cur[i] = res_nxt[i];
+#ifdef FIM_TIMING
+    const unsigned long long _t4 = wall_clock64();
+    ph[0] += _t1 - _t0; ph[1] += _t2 - _t1; ph[2] += _t3 - _t2; ph[3] += _t4 - _t3;
+#endif
   }
+#ifdef FIM_TIMING
+  if (tid == 0 && blockIdx.x < 1024) {
+    for (int k = 0; k < 4; ++k) fim_mlp_timing[blockIdx.x][k] = ph[k];
+  }
+  (void)t_begin;
+#endif
 }
+#ifdef FIM_TIMING
+extern "C" int fim_debug_mlp_timing(void* dst) {
+  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(fim_mlp_timing), sizeof(fim_mlp_timing), 0, hipMemcpyDeviceToHost);
+}
+#endif
 
 }  // namespace fim
 
