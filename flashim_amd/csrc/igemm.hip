@@ -129,10 +129,111 @@ __device__ __forceinline__ int pixel_of_row(const ConvArgs& a, int m, int& img, 
 // lane = pixel (lane & 15) of a 16-pixel block and 4 consecutive channels 4 (lane >> 4) + v of a 16-channel block, so
 // each store writes 4 channels of one pixel. row0: the wave's first GEMM row; n_tile0: the tile's first channel; nl0:
 // the wave's first channel within the tile (index into the per-channel operands ep_* staged in LDS).
+// Branch-free epilogue for the common case (no residual, no pooling, Cout % 16 == 0, output below 2 GiB): every value
+// of the wave is computed before the first store, so the per-value chains (GELU's above all) interleave, and outputs
+// past M or Cout are dropped by the buffer store's range check instead of per-lane branches. Same arithmetic, in the
+// same order per value, as the general epilogue below.
+template <int KIND, int OUT, int MB, int NB, bool GELU>
+__device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
+                                                   const v4f (&acc_f)[NB][MB], int row0, int n_tile0, int nl0,
+                                                   const float* ep_scale, const float* ep_bias, const float* ep_oinv) {
+  constexpr int ESZ = OUT == OUT_BF16 ? 2 : 1;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4;
+  const float out_scale = OUT == OUT_INT8 ? *a.out_scale : 1.0f;
+  const float out_inv = OUT == OUT_INT8 ? __fdiv_rn(1.0f, out_scale) : 1.0f;
+  const bool has_bias = a.bias != nullptr;
+  const bool relu_pre = a.relu_pre != 0;
+  const bool row_scales = KIND == KIND_INT8 && a.a_scale_rows != nullptr;
+  const uint32_t nbytes = (uint32_t)a.M * (uint32_t)a.Cout * ESZ;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(a.out, (short)0, (int)nbytes, 0x00020000);
+  float arow[MB];
+#pragma unroll
+  for (int j = 0; j < MB; ++j) arow[j] = row_scales ? a.a_scale_rows[min(row0 + j * 16 + (lane & 15), a.M - 1)] : 1.f;
+  float y[NB][MB][4];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int nl = nl0 + i * 16 + 4 * g;
+    const float4 cs4 = *reinterpret_cast<const float4*>(&ep_scale[nl]);
+    const float4 cb4 = *reinterpret_cast<const float4*>(&ep_bias[nl]);
+    const float cs[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
+    const float cb[4] = {cb4.x, cb4.y, cb4.z, cb4.w};
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      float* v = y[i][j];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float t;
+        if (KIND == KIND_INT8)
+          t = row_scales ? __fmul_rn((float)acc_i[i][j][e], __fmul_rn(arow[j], cs[e]))
+                         : __fmul_rn((float)acc_i[i][j][e], cs[e]);
+        else
+          t = acc_f[i][j][e];
+        t = has_bias ? __fadd_rn(t, cb[e]) : t;
+        v[e] = relu_pre ? fmaxf(t, 0.0f) : t;
+      }
+      round_bf16x2(v[0], v[1]);
+      round_bf16x2(v[2], v[3]);
+#ifdef FIM_EPI_NOGELU
+      if (false) {
+#else
+      if (GELU) {
+#endif
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
+        round_bf16x2(v[0], v[1]);
+        round_bf16x2(v[2], v[3]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int nl = nl0 + i * 16 + 4 * g;
+    const int nbase = n_tile0 + nl;
+    const bool nvalid = n_tile0 + nl0 + i * 16 < a.Cout;  // whole 16-channel block in or out (Cout % 16 == 0)
+    const float4 ci4 = *reinterpret_cast<const float4*>(&ep_oinv[nl]);
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const float* v = y[i][j];
+      const int m = row0 + j * 16 + (lane & 15);
+#ifdef FIM_EPI_NOSTORE
+      if (v[0] + v[1] + v[2] + v[3] == 12345.0f) static_cast<uint16_t*>(a.out)[m] = 1;
+      continue;
+#endif
+      // rows past M land past the buffer's end; invalid channel blocks are sent there too
+      const uint32_t off = nvalid ? ((uint32_t)m * (uint32_t)a.Cout + (uint32_t)nbase) * ESZ : 0x80000000u;
+      if (OUT == OUT_BF16) {
+        const uint32_t lo = pack_bf16x2(v[0], v[1]), hi = pack_bf16x2(v[2], v[3]);
+        typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rsrc, (int)off, 0, 0);
+      } else {
+        uint32_t pk;
+        if (OUT == OUT_INT8) {
+          pk = 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) pk |= (uint32_t)(uint8_t)quantize_int8_fast(v[e], out_scale, out_inv) << (8 * e);
+        } else {
+          pk = pack_e4m3x4(mx_scale_clamp(v[0], ci4.x), mx_scale_clamp(v[1], ci4.y), mx_scale_clamp(v[2], ci4.z),
+                           mx_scale_clamp(v[3], ci4.w));
+        }
+        __builtin_amdgcn_raw_buffer_store_b32(pk, rsrc, (int)off, 0, 0);
+      }
+    }
+  }
+}
+
 template <int KIND, int OUT, int POOL, int MB, int NB>
 __device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc_i)[NB][MB], const v4f (&acc_f)[NB][MB],
                                               int row0, int n_tile0, int nl0, const float* ep_scale,
                                               const float* ep_bias, const float* ep_oinv) {
+  if (!POOL && a.residual == nullptr && (a.Cout & 15) == 0 &&
+      (int64_t)a.M * a.Cout * (OUT == OUT_BF16 ? 2 : 1) < (int64_t)0x7fffffff) {
+    if (a.gelu)
+      conv_epilogue_fast<KIND, OUT, MB, NB, true>(a, acc_i, acc_f, row0, n_tile0, nl0, ep_scale, ep_bias, ep_oinv);
+    else
+      conv_epilogue_fast<KIND, OUT, MB, NB, false>(a, acc_i, acc_f, row0, n_tile0, nl0, ep_scale, ep_bias, ep_oinv);
+    return;
+  }
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4;
   // flags are uniform (scalar branches); the output format is a template parameter
@@ -296,9 +397,9 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc
 
 template <int KIND, int BN, int LW, int OUT, int XS, int POOL>
 __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
-  constexpr int SXN = XS ? 4 : 1;        // activation scale registers per set: one per 16-pixel block with row scales
-  constexpr int NB = BN / 32;            // 16-channel blocks per wavefront (BN/2 channels)
   constexpr int MB = 4;                  // 16-pixel blocks per wavefront (64 pixels)
+  constexpr int SXN = XS ? MB : 1;       // activation scale registers per set: one per 16-pixel block with row scales
+  constexpr int NB = BN / 32;            // 16-channel blocks per wavefront (BN/2 channels)
   constexpr int A_PASSES = BM / 32;      // 256 lanes x 16 B cover 32 rows x 128 B per pass
   constexpr int B_PASSES = BN / 32;
   constexpr int STAGE = (BM + BN) * KC;  // pixel rows first, then weight rows; 128 B per row, XOR-swizzled
@@ -484,27 +585,41 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) sw[i] = blk_ok ? rsw[i] + 127 : 127;
     const uint8_t* st = lds + buf * STAGE;
-    v4i xlo[MB], xhi[MB];
+    if constexpr (KIND == KIND_INT8) {
+      v4i xlo[MB], xhi[MB];
 #pragma unroll
-    for (int i = 0; i < MB; ++i) {
-      xlo[i] = *reinterpret_cast<const v4i*>(st + fr_x[i]);
-      xhi[i] = *reinterpret_cast<const v4i*>(st + (fr_x[i] ^ 64));
-    }
+      for (int i = 0; i < MB; ++i) {
+        xlo[i] = *reinterpret_cast<const v4i*>(st + fr_x[i]);
+        xhi[i] = *reinterpret_cast<const v4i*>(st + (fr_x[i] ^ 64));
+      }
 #pragma unroll
-    for (int i = 0; i < NB; ++i) {
-      const v4i wlo = *reinterpret_cast<const v4i*>(st + fr_w[i]);
-      const v4i whi = *reinterpret_cast<const v4i*>(st + (fr_w[i] ^ 64));
+      for (int i = 0; i < NB; ++i) {
+        const v4i wlo = *reinterpret_cast<const v4i*>(st + fr_w[i]);
+        const v4i whi = *reinterpret_cast<const v4i*>(st + (fr_w[i] ^ 64));
 #pragma unroll
-      for (int j = 0; j < MB; ++j) {
-        if (KIND == KIND_INT8) {
+        for (int j = 0; j < MB; ++j) {
           acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wlo, xlo[j], acc_i[i][j], 0, 0, 0);
           acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(whi, xhi[j], acc_i[i][j], 0, 0, 0);
-        } else {
-          const v8i wf = v8i{wlo[0], wlo[1], wlo[2], wlo[3], whi[0], whi[1], whi[2], whi[3]};
-          const v8i xf = v8i{xlo[j][0], xlo[j][1], xlo[j][2], xlo[j][3], xhi[j][0], xhi[j][1], xhi[j][2], xhi[j][3]};
-          acc_f[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf, xf, acc_f[i][j], 0, 0, 0, sw[i], 0,
-                                                                         sxs[j]);
         }
+      }
+    } else {
+      // each operand is built once as the 8-register tuple the MFMA reads, straight from its two LDS reads
+      v8i xf[MB];
+#pragma unroll
+      for (int j = 0; j < MB; ++j) {
+        const v4i lo = *reinterpret_cast<const v4i*>(st + fr_x[j]);
+        const v4i hi = *reinterpret_cast<const v4i*>(st + (fr_x[j] ^ 64));
+        xf[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const v4i lo = *reinterpret_cast<const v4i*>(st + fr_w[i]);
+        const v4i hi = *reinterpret_cast<const v4i*>(st + (fr_w[i] ^ 64));
+        const v8i wf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+        for (int j = 0; j < MB; ++j)
+          acc_f[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf, xf[j], acc_f[i][j], 0, 0, 0, sw[i], 0,
+                                                                         sxs[j]);
       }
     }
   };
