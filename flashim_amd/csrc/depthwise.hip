@@ -183,9 +183,11 @@ __global__ __launch_bounds__(256) void dw5x5_kernel(const DwArgs a) {
           round_bf16x2(y[0], y[1]);
           round_bf16x2(y[2], y[3]);
         }
+        int qi[4];
+        quantize_int8_fast_n<4>(y, oscale, oinv8, qi);
         uint32_t q = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) q |= (uint32_t)(uint8_t)quantize_int8_fast(y[i], oscale, oinv8) << (8 * i);
+        for (int i = 0; i < 4; ++i) q |= (uint32_t)(uint8_t)qi[i] << (8 * i);
         *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.out) + row * a.C + c) = q;
       } else if (OUT == DW_MX_STATIC) {
         const uint32_t q = pack_e4m3x4(mx_scale_clamp(y[0], oinv), mx_scale_clamp(y[1], oinv),

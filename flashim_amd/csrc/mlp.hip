@@ -186,9 +186,10 @@ __global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int h0 = 64 * wave + 16 * i + 4 * g;  // this lane's 4 output channels
+        float yb[4][4];  // the block's 16 values, all computed before any is quantized (one INT8 tie test)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          float y[4];
+          float (&y)[4] = yb[j];
           if (KIND == MLP_INT8) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) y[v] = __fadd_rn(__fmul_rn((float)acc_i[i][j][v], s1[h0 + v]), b1s[h0 + v]);
@@ -213,17 +214,26 @@ __global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
 #endif
           round_bf16x2(y[0], y[1]);
           round_bf16x2(y[2], y[3]);
-          uint32_t q;
-          if (KIND == MLP_MX) {
-            q = pack_e4m3x4(mx_scale_clamp(y[0], hinv[h0]), mx_scale_clamp(y[1], hinv[h0 + 1]),
-                            mx_scale_clamp(y[2], hinv[h0 + 2]), mx_scale_clamp(y[3], hinv[h0 + 3]));
-          } else {
-            q = 0;
+        }
+        uint32_t qw[4];
+        if (KIND == MLP_MX) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) q |= (uint32_t)(uint8_t)quantize_int8_fast(y[v], hq_scale, hq_inv) << (8 * v);
-          }
+          for (int j = 0; j < 4; ++j)
+            qw[j] = pack_e4m3x4(mx_scale_clamp(yb[j][0], hinv[h0]), mx_scale_clamp(yb[j][1], hinv[h0 + 1]),
+                                mx_scale_clamp(yb[j][2], hinv[h0 + 2]), mx_scale_clamp(yb[j][3], hinv[h0 + 3]));
+        } else {
+          const float (&flat)[16] = reinterpret_cast<const float (&)[16]>(yb);
+          int qi[16];
+          quantize_int8_fast_n<16>(flat, hq_scale, hq_inv, qi);
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            qw[j] = (uint32_t)(uint8_t)qi[4 * j] | ((uint32_t)(uint8_t)qi[4 * j + 1] << 8) |
+                    ((uint32_t)(uint8_t)qi[4 * j + 2] << 16) | ((uint32_t)(uint8_t)qi[4 * j + 3] << 24);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
           const int px = 16 * j + r16;
-          *reinterpret_cast<uint32_t*>(&hs[px * MLP_H + ((((h0 >> 4)) ^ (px & 15)) << 4) + (h0 & 15)]) = q;
+          *reinterpret_cast<uint32_t*>(&hs[px * MLP_H + ((((h0 >> 4)) ^ (px & 15)) << 4) + (h0 & 15)]) = qw[j];
         }
       }
     }

@@ -180,6 +180,33 @@ __device__ __forceinline__ int8_t quantize_int8_fast(float x, float scale, float
   q = q < -127.0f ? -127.0f : q;
   return (int8_t)(int)q;
 }
+
+// quantize_int8_fast of N values with one near-tie test for all of them: a single wave-uniform branch instead of one
+// per value, so the code producing the N inputs is not split by branches (each value's result is unchanged).
+template <int N>
+__device__ __forceinline__ void quantize_int8_fast_n(const float (&x)[N], float scale, float inv, int (&q)[N]) {
+  float y[N];
+  bool near[N];
+  bool any = false;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    y[i] = x[i] * inv;
+    near[i] = fabsf(y[i] - __builtin_floorf(y[i]) - 0.5f) <= 0x1p-15f;
+    any = any || near[i];
+  }
+  if (__builtin_amdgcn_ballot_w64(any) != 0) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (near[i]) y[i] = __fdiv_rn(x[i], scale);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    float r = __builtin_rintf(y[i]);
+    r = r > 127.0f ? 127.0f : r;
+    r = r < -127.0f ? -127.0f : r;
+    q[i] = (int)r;
+  }
+}
 #endif
 
 // One element of quantize_blocks + .to(float8_e4m3fn): clamp(x / 2^e, +-448) -> E4M3. Division by an exact power of
