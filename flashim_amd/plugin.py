@@ -74,6 +74,26 @@ def _eligible_mxfp8_linear(activation, bias, weight) -> bool:
     return _gemm.eligible_mxfp8_linear(act, bias, wgt)
 
 
+def _as_local_weight(weight):
+    from flashim_amd import quant
+
+    return quant.QuantizedWeight(weight.values, weight.scale_exponent, tuple(weight.logical_shape))
+
+
+def _mxfp8_gelu_mlp(x, w1, b1, hidden_exponent, w2):
+    act, lw1 = _as_local(x, w1)
+    return _gemm.mxfp8_gelu_mlp(act, lw1, b1, hidden_exponent, _as_local_weight(w2))
+
+
+def _eligible_mxfp8_gelu_mlp(x, w1, b1, hidden_exponent, w2) -> bool:
+    try:
+        act, lw1 = _as_local(x, w1)
+        lw2 = _as_local_weight(w2)
+    except (AttributeError, ValueError, TypeError):
+        return False
+    return _gemm.eligible_mxfp8_gelu_mlp(act, lw1, b1, hidden_exponent, lw2)
+
+
 def impls(upstream_tensor_module) -> dict[str, tuple[Callable, Callable]]:
     """``{op name: (impl, when)}`` for the FlashIM ops this backend replaces."""
     quantize_mxfp8, quantize_int8 = _adapt_quantized(upstream_tensor_module)
@@ -92,6 +112,7 @@ def impls(upstream_tensor_module) -> dict[str, tuple[Callable, Callable]]:
         "int8_linear": (_gemm.int8_linear, _gemm.eligible_int8_linear),
         "mxfp8_scaled_mm": (_gemm.mxfp8_scaled_mm, _gemm.eligible_mxfp8_scaled_mm),
         "mxfp8_linear": (_mxfp8_linear, _eligible_mxfp8_linear),
+        "mxfp8_gelu_mlp": (_mxfp8_gelu_mlp, _eligible_mxfp8_gelu_mlp),
     }
 
 
