@@ -58,6 +58,7 @@ struct ConvArgs {
   int M;                   // output pixels (< 2^31)
   int kchunks;             // ceil(Cin / 128)
   int n_tiles, m_tiles;
+  int m_base;              // first GEMM row of this launch (a split launch runs its last rows as a second launch)
 };
 
 #ifdef FIM_TIMING
@@ -71,7 +72,7 @@ extern "C" int fim_debug_timing(void* dst) {
 #define FIM_STAMP(k) do { } while (0)
 #endif
 
-constexpr int BM = 128;
+constexpr int BM_MAIN = 128;  // pixel rows per tile (the tail of a launch may use 64-row tiles)
 constexpr int KC = 128;          // bytes of K per step
 
 
@@ -395,9 +396,10 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc
   }
 }
 
-template <int KIND, int BN, int LW, int OUT, int XS, int POOL>
+template <int KIND, int BN, int LW, int OUT, int XS, int POOL, int MBW = 4>
 __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
-  constexpr int MB = 4;                  // 16-pixel blocks per wavefront (64 pixels)
+  constexpr int MB = MBW;                // 16-pixel blocks per wavefront (64 pixels; 32 in the tail's small tiles)
+  constexpr int BM = 32 * MB;            // pixel rows per tile: two wavefronts of MB blocks
   constexpr int SXN = XS ? MB : 1;       // activation scale registers per set: one per 16-pixel block with row scales
   constexpr int NB = BN / 32;            // 16-channel blocks per wavefront (BN/2 channels)
   constexpr int A_PASSES = BM / 32;      // 256 lanes x 16 B cover 32 rows x 128 B per pass
@@ -419,7 +421,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
   const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
   if (t >= a.n_tiles * a.m_tiles) return;
   const int n0 = (t % a.n_tiles) * BN;
-  const int m0 = (t / a.n_tiles) * BM;
+  const int m0 = a.m_base + (t / a.n_tiles) * BM;
 
   // per-channel epilogue operands, staged once (their loads overlap the prologue; the prologue barrier orders them)
   if (tid < BN) {
@@ -478,7 +480,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
   int fr_x[MB], fr_w[NB];
 #pragma unroll
   for (int i = 0; i < MB; ++i) {
-    const int r = wm * 64 + i * 16 + (lane & 15);
+    const int r = wm * (MB * 16) + i * 16 + (lane & 15);
     fr_x[i] = r * KC + ((g ^ ((r >> 1) & 7)) << 4);
   }
 #pragma unroll
@@ -529,7 +531,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
       } else {
 #pragma unroll
         for (int j = 0; j < SXN; ++j) {
-          int r = m0 + wm * 64 + j * 16 + (lane & 15);
+          int r = m0 + wm * (MB * 16) + j * 16 + (lane & 15);
           r = r < a.M ? r : a.M - 1;
           const int rt = r & 127;
           pre_sx[j] = (int)a.x_swz[(((int64_t)(r >> 7) * a.x_swz_tiles_k + (cblk >> 2)) << 9) + (rt & 31) * 16 +
@@ -664,10 +666,27 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
   }
 
   FIM_STAMP(2);
-  conv_epilogue<KIND, OUT, POOL, MB, NB>(a, acc_i, acc_f, m0 + wm * 64, n0, wn * (BN / 2), ep_scale, ep_bias, ep_oinv);
+  conv_epilogue<KIND, OUT, POOL, MB, NB>(a, acc_i, acc_f, m0 + wm * (MB * 16), n0, wn * (BN / 2), ep_scale, ep_bias, ep_oinv);
   FIM_STAMP(3);
 }
 
+
+// The tail of a split launch: 64 x 64 tiles (2 x 2 blocks per wavefront) on the plain path.
+template <int KIND>
+static void launch_tail(const ConvArgs& a, int lw, dim3 grid, hipStream_t stream) {
+  constexpr int QOUT = KIND == KIND_INT8 ? OUT_INT8 : OUT_E4M3;
+  if (a.out_mode == OUT_BF16) {
+    if (lw == 16)
+      conv_igemm_kernel<KIND, 64, 16, OUT_BF16, 0, 0, 2><<<grid, dim3(256), 0, stream>>>(a);
+    else
+      conv_igemm_kernel<KIND, 64, 1, OUT_BF16, 0, 0, 2><<<grid, dim3(256), 0, stream>>>(a);
+  } else {
+    if (lw == 16)
+      conv_igemm_kernel<KIND, 64, 16, QOUT, 0, 0, 2><<<grid, dim3(256), 0, stream>>>(a);
+    else
+      conv_igemm_kernel<KIND, 64, 1, QOUT, 0, 0, 2><<<grid, dim3(256), 0, stream>>>(a);
+  }
+}
 
 template <int KIND, int BN, int OUT, int XS, int POOL = 0>
 static void launch_lw(const ConvArgs& a, int lw, dim3 grid, hipStream_t stream) {
@@ -725,10 +744,36 @@ static int launch_conv(ConvArgs a, hipStream_t stream) {
   if (a.Cin % 16 == 0 && both % 16 == 0) lw = 16;
   const int bn = (a.Cout > 64 && a.x_swz == nullptr) ? 128 : 64;
   a.n_tiles = (a.Cout + bn - 1) / bn;
-  const int64_t m_tiles = (a.M + BM - 1) / BM;
+  const int64_t m_tiles = (a.M + BM_MAIN - 1) / BM_MAIN;
   const int64_t tiles = m_tiles * a.n_tiles;
   if (tiles > (1LL << 30)) return FIM_ERR_UNSUPPORTED;
   a.m_tiles = (int)m_tiles;
+  a.m_base = 0;
+  // Workgroups stay resident 2 per CU, so tiles run in rounds of 2 x CUs. When the last round would be less than half
+  // full (e.g. config 2: 632 tiles on 512 slots), it would still take a full tile time: the whole M tiles that fill
+  // complete rounds run as one launch and the remaining rows as a second launch of 64 x 64 tiles (4x as many, each
+  // about a quarter of the work), which fills the last round instead.
+  if (a.x_swz == nullptr && a.pool_out == nullptr) {
+    const int64_t slots = 2LL * device_cus();
+    const int64_t full = tiles / slots, rem = tiles - full * slots;
+    const int64_t mt_main = full * slots / a.n_tiles;
+    if (full > 0 && rem > 0 && rem * 2 < slots && mt_main > 0 && mt_main < m_tiles) {
+      ConvArgs t = a;
+      a.m_tiles = (int)mt_main;
+      const dim3 g1((unsigned)(cdiv(mt_main * a.n_tiles, 8) * 8));
+      if (bn == 128)
+        launch_xs<KIND, 128>(a, lw, g1, stream);
+      else
+        launch_xs<KIND, 64>(a, lw, g1, stream);
+      const int status = launch_status();
+      if (status != FIM_OK) return status;
+      t.m_base = (int)(mt_main * BM_MAIN);
+      t.n_tiles = (a.Cout + 63) / 64;
+      t.m_tiles = (int)cdiv(a.M - t.m_base, 64);
+      launch_tail<KIND>(t, lw, dim3((unsigned)(cdiv((int64_t)t.m_tiles * t.n_tiles, 8) * 8)), stream);
+      return launch_status();
+    }
+  }
   dim3 grid((unsigned)(cdiv(tiles, 8) * 8));  // a multiple of the 8 XCDs: the kernel maps pids to tiles per XCD
   if (bn == 128)
     launch_xs<KIND, 128>(a, lw, grid, stream);

@@ -231,3 +231,35 @@ def test_int8_conv2d_maxpool_bit_exact(shape, cin, cout, geo, relu):
     assert out.shape == want_out.shape and pooled.shape == want_pooled.shape and pooled.dtype == torch.int8
     assert torch.equal(out.cpu(), want_out)
     assert torch.equal(pooled.cpu(), want_pooled)
+
+
+@pytest.mark.parametrize("kind", ["int8", "mxfp8"])
+def test_split_launch_tail(kind):
+    """More tiles than two rounds of resident workgroups, the last round mostly empty: 1x1, 64 -> 192 channels on
+    1 x 260 x 256 pixels = 520 M tiles x 2 N tiles = 1040 tiles on 512 slots (2 per CU on 256 CUs), so rows from 65536
+    on run as a second launch of 64 x 64 tiles (3 N tiles). A 1x1 conv's rows are independent: every row must equal,
+    bit for bit, the same rows from launches on 4-row slices of the image (too small to split; the same MFMA per
+    16 x 16 block and the same epilogue). Plus the oracle bar (INT8 bit-exact; MXFP8 with GELU: relative L2)."""
+    torch.manual_seed(11)
+    geo = (1, 1, 1, 1, 0, 0, 1, 1)
+    if kind == "int8":
+        x = torch.randint(-127, 127, (1, 260, 256, 64), dtype=torch.int8)
+        w = torch.randint(-127, 127, (192, 64), dtype=torch.int8)
+        a_scale, w_scale = torch.tensor(0.013), torch.rand(192) * 0.01 + 0.001
+        bias = torch.randn(192).to(torch.bfloat16)
+        run = lambda xs: ops.int8_conv2d.get("hip")(*_dev(xs, w, a_scale, w_scale, bias), *geo, relu=True).cpu()  # noqa: E731
+        got = run(x)
+        assert torch.equal(got, ref.int8_conv2d(x, w, a_scale, w_scale, bias, *geo, relu=True))
+    else:
+        x = (torch.randn(1, 260, 256, 64) * 3).to(torch.float8_e4m3fn)
+        ce = torch.randint(-6, 3, (2,), dtype=torch.int8)
+        w = (torch.randn(192, 64) * 2).to(torch.float8_e4m3fn)
+        we = torch.randint(-9, -3, (192, 2), dtype=torch.int8)
+        bias = torch.randn(192).to(torch.bfloat16)
+        run = lambda xs: ops.mxfp8_conv2d.get("hip")(*_dev(xs, ce, w, we, bias), *geo, gelu=True).cpu()  # noqa: E731
+        got = run(x)
+        want = ref.mxfp8_conv2d(x, ce, w, we, bias, *geo, gelu=True).float()
+        assert (got.float() - want).norm() / want.norm() <= 1e-3
+    for r0 in (0, 128, 254, 256):  # slices in the first launch, across the boundary row 65536 = 256 x 256, the tail
+        sl = run(x[:, r0:r0 + 4].contiguous())
+        assert torch.equal(got[:, r0:r0 + 4].view(torch.int16), sl.view(torch.int16)), r0
