@@ -41,7 +41,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--only", default=None, help="run one workload only (cfg1|cfg2|cfg3|cfg3q|dw|cfg4|cfg5int8|cfg5mxfp8|copy)"
+    p.add_argument("--only", default=None, help="run one workload only (cfg1|cfg2|cfg3|cfg3q|dw|stem|cfg4|cfg5int8|cfg5mxfp8|copy)"
                                                   " and print its line (profiling runs)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-stack", action="store_true", help="skip configs 4 and 5")
@@ -180,6 +180,23 @@ def cfg4_depthwise():
     return fn, {"bytes": pixels * 64 * 2 + pixels * 64}
 
 
+def stem():
+    """The VGG stem (conv2d_small_cin_quantize_int8): 3 x 3 conv of a BF16 NCHW 1 x 3 x 896 x 1200 image, 3 -> 64,
+    + bias + ReLU -> static INT8 NHWC (the image size FlashIM times its own kernel on, flashim/backends/triton/conv.py
+    :916-917). HBM bytes: 2 per input element + 1 per output code."""
+    from flashim_amd import ops
+
+    g = torch.Generator(device="cpu").manual_seed(9)
+    x = torch.randn(1, 3, 896, 1200, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(64, 3, 3, 3, generator=g) * 0.3).to(torch.bfloat16).to(DEV)
+    b = torch.randn(64, generator=g).to(torch.bfloat16).to(DEV)
+    scale = torch.tensor(0.04, device=DEV)
+    bound = ops.conv2d_small_cin_quantize_int8.bind(w, b)
+    fn = lambda: bound(x, scale)  # noqa: E731
+    pixels = 896 * 1200
+    return fn, {"bytes": pixels * 3 * 2 + pixels * 64}
+
+
 def copy_calibration():
     """A plain device copy of a known size (the PMC traffic calibration)."""
     src = torch.empty(64 << 20, device=DEV, dtype=torch.uint8).fill_(1)
@@ -268,6 +285,9 @@ def main() -> int:
     if only in (None, "dw"):
         fn, info = cfg4_depthwise()
         hbm_line("cfg4_depthwise_gelu_mxfp8", fn, info)
+    if only in (None, "stem"):
+        fn, info = stem()
+        hbm_line("stem_conv3x3_cin3_int8", fn, info)
     if not a.no_stack and only in (None, "cfg4", "cfg5int8", "cfg5mxfp8"):
         from flashim_amd import blocks
 

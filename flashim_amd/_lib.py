@@ -50,6 +50,8 @@ SIGNATURES: dict[str, list] = {
     "fim_im2col_gather": [_vp, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp],
     "fim_refiner_mlp": [_i32, _i32, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _vp,
                         _vp],
+    "fim_conv3x3_small_cin_quantize_int8": [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _vp],
+    "fim_bias_relu_quantize_int8": [_vp, _i64, _i64, _i64, _i64, _vp, _i32, _vp, _vp, _vp],
     "fim_depthwise5x5": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp],
     "fim_test_e4m3": [_vp, _i64, _vp, _vp],
     "fim_test_mx_exponent": [_vp, _i64, _vp, _vp],

@@ -5,6 +5,8 @@
 * ``depthwise5x5_relu_mxfp8`` / ``depthwise5x5_relu_int8`` (``flashim/ops/conv.py:30-61``) -> ``fim_depthwise5x5``
 * ``depthwise5x5_gelu`` (this backend's refiner-block producer: folded BatchNorm + GELU, BF16 / static INT8 / static
   MXFP8 out) -> ``fim_depthwise5x5``
+* ``conv2d_small_cin_quantize_int8`` (``flashim/ops/conv.py:225-235``) -> ``fim_conv3x3_small_cin_quantize_int8``
+* ``bias_relu_quantize_int8`` (``flashim/ops/quantize.py:134-142``) -> ``fim_bias_relu_quantize_int8``
 
 ``gelu=`` on the two convs is an epilogue FlashIM's conv ops do not have: it is ``int8_linear``'s GELU
 (``flashim/ops/gemm.py:94-95``): ``F.gelu`` of the BF16 result, rounded to BF16, before the residual.
@@ -291,3 +293,71 @@ def eligible_pointwise_int8(value, dw_weight, dw_bias, pw_weight, pw_wscale, pw_
         eligible_depthwise(value, dw_weight, dw_bias) and pw_weight.dtype == torch.int8 and pw_weight.ndim == 2
         and pw_weight.shape[1] == value.shape[1] and pw_wscale.numel() == pw_weight.shape[0] and scale.numel() == 1
     )
+
+
+# -- the VGG stem: conv2d_small_cin_quantize_int8 (flashim/ops/conv.py:225-235) and its epilogue alone,
+# bias_relu_quantize_int8 (flashim/ops/quantize.py:134-142) ------------------------------------------------------
+
+STEM_MAX_CIN = 8
+
+
+def small_cin_prepare(weight: Tensor, bias: Tensor) -> tuple[Tensor, Tensor]:
+    """``[Cout, Cin, 3, 3]`` -> BF16 ``[Cout, KP]``: taps in (c, ky, kx) order, zero-padded to KP = 32 ceil(9 Cin / 32)
+    (the MFMA's K step); ``bias`` unchanged."""
+    cout, cin = weight.shape[:2]
+    taps = 9 * cin
+    kp = -(-taps // 32) * 32
+    packed = torch.nn.functional.pad(weight.detach().to(torch.bfloat16).reshape(cout, taps), (0, kp - taps))
+    return packed.contiguous(), bias.detach()
+
+
+def conv2d_small_cin_quantize_int8(x: Tensor, scale: Tensor, packed: Tensor, bias: Tensor) -> quant.Int8Tensor:
+    """``quantize_int8(relu(bf16(conv3x3(x)) + bias))`` -> INT8 NHWC ``[B, H, W, Cout]`` (an :class:`Int8Tensor` with
+    ``scale``); ``packed`` from :func:`small_cin_prepare`."""
+    b, cin, h, w = x.shape
+    cout = packed.shape[0]
+    x = x.contiguous()
+    packed = packed.to(x.device).contiguous()
+    bias_t, code = _bias_args(bias, x.device)
+    scale_t = scale.to(device=x.device, dtype=torch.float32).reshape(1).contiguous()
+    out = torch.empty(b, h, w, cout, device=x.device, dtype=torch.int8)
+    _lib.call("fim_conv3x3_small_cin_quantize_int8", x.data_ptr(), b, cin, h, w, packed.data_ptr(), cout,
+              bias_t.data_ptr(), code, scale_t.data_ptr(), out.data_ptr(), _lib.stream_of(x),
+              what=f"conv2d_small_cin_quantize_int8 {tuple(x.shape)} -> {cout}")
+    return quant.Int8Tensor(out, scale)
+
+
+def eligible_small_cin(x: Tensor, scale: Tensor, weight: Tensor, bias: Tensor) -> bool:
+    return (
+        isinstance(x, Tensor) and x.ndim == 4 and x.dtype == torch.bfloat16 and x.is_contiguous() and is_gfx950(x.device)
+        and weight.dtype == torch.bfloat16 and bias.dtype in (torch.bfloat16, torch.float32) and scale.numel() == 1
+        and x.shape[1] == weight.shape[1]
+    )
+
+
+def accepts_small_cin(weight: Tensor, bias: Tensor) -> bool:
+    cout = weight.shape[0]
+    return (
+        weight.ndim == 4 and tuple(weight.shape[2:]) == (3, 3) and 1 <= weight.shape[1] <= STEM_MAX_CIN
+        and 16 <= cout <= 128 and cout & (cout - 1) == 0 and tuple(bias.shape) == (cout,)
+    )
+
+
+def bias_relu_quantize_int8(raw: Tensor, bias: Tensor, scale: Tensor) -> quant.Int8Tensor:
+    """``quantize_int8(relu(raw + bias))`` of a BF16 NCHW conv output -> INT8 NHWC ``[B, H, W, C]``."""
+    b, c, h, w = raw.shape
+    raw = raw.contiguous()
+    bias_t, code = _bias_args(bias, raw.device)
+    scale_t = scale.to(device=raw.device, dtype=torch.float32).reshape(1).contiguous()
+    out = torch.empty(b, h, w, c, device=raw.device, dtype=torch.int8)
+    _lib.call("fim_bias_relu_quantize_int8", raw.data_ptr(), b, c, h, w, bias_t.data_ptr(), code, scale_t.data_ptr(),
+              out.data_ptr(), _lib.stream_of(raw), what=f"bias_relu_quantize_int8 {tuple(raw.shape)}")
+    return quant.Int8Tensor(out, scale)
+
+
+def eligible_bias_relu_quantize(raw: Tensor, bias: Tensor, scale: Tensor) -> bool:
+    return (
+        isinstance(raw, Tensor) and raw.ndim == 4 and raw.dtype == torch.bfloat16 and is_gfx950(raw.device)
+        and bias.dtype in (torch.bfloat16, torch.float32) and bias.numel() == raw.shape[1] and scale.numel() == 1
+    )
+

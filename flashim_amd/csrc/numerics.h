@@ -165,47 +165,38 @@ FIM_HD int8_t quantize_int8_value(float x, float scale) {
 #ifdef __HIPCC__
 // quantize_int8_value with the division replaced by a multiply by inv = 1 / scale (correctly rounded), falling back
 // to the IEEE division only where it can matter: x * inv is within a few ulps of the exact quotient, so both round to
-// the same integer unless the quotient sits within 2^-15 of a half-integer (|q| < 128; beyond, both saturate). The
-// fallback sits behind a wave-uniform branch (taken when any lane of the wavefront is near a tie, ~0.4% of the
-// time), so the division is not evaluated for every element.
-__device__ __forceinline__ int8_t quantize_int8_fast(float x, float scale, float inv) {
-  float y = x * inv;
-  const float fr = y - __builtin_floorf(y);
-  const bool near = fabsf(fr - 0.5f) <= 0x1p-15f;
-  if (__builtin_amdgcn_ballot_w64(near) != 0) {
-    if (near) y = __fdiv_rn(x, scale);
-  }
-  float q = __builtin_rintf(y);
-  q = q > 127.0f ? 127.0f : q;
-  q = q < -127.0f ? -127.0f : q;
-  return (int8_t)(int)q;
-}
-
-// quantize_int8_fast of N values with one near-tie test for all of them: a single wave-uniform branch instead of one
-// per value, so the code producing the N inputs is not split by branches (each value's result is unchanged).
-template <int N>
+// the same integer unless the quotient sits within 2^-15 of a half-integer, i.e. |t - rint(t)| >= 0.5 - 2^-15 for
+// t = x * inv (t - rint(t) is exact); beyond |q| = 127 both saturate. The fallback sits behind one wave-uniform branch
+// for all N values (taken when any lane is near a tie), so it neither runs per element nor splits the code that
+// produces the inputs. The saturation is one v_med3_f32 (LO = 0 folds a preceding ReLU in: relu then quantize equals
+// clamping the rounded quotient at 0). Checked on the host against round(x / s) on 20M cases including exact ties and
+// their neighbours, with and without the ReLU.
+template <int N, int LO = -127>
 __device__ __forceinline__ void quantize_int8_fast_n(const float (&x)[N], float scale, float inv, int (&q)[N]) {
-  float y[N];
+  float r[N];
   bool near[N];
   bool any = false;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    y[i] = x[i] * inv;
-    near[i] = fabsf(y[i] - __builtin_floorf(y[i]) - 0.5f) <= 0x1p-15f;
+    const float t = x[i] * inv;
+    r[i] = __builtin_rintf(t);
+    near[i] = fabsf(t - r[i]) >= 0.5f - 0x1p-15f;
     any = any || near[i];
   }
   if (__builtin_amdgcn_ballot_w64(any) != 0) {
 #pragma unroll
     for (int i = 0; i < N; ++i)
-      if (near[i]) y[i] = __fdiv_rn(x[i], scale);
+      if (near[i]) r[i] = __builtin_rintf(__fdiv_rn(x[i], scale));
   }
 #pragma unroll
-  for (int i = 0; i < N; ++i) {
-    float r = __builtin_rintf(y[i]);
-    r = r > 127.0f ? 127.0f : r;
-    r = r < -127.0f ? -127.0f : r;
-    q[i] = (int)r;
-  }
+  for (int i = 0; i < N; ++i) q[i] = (int)__builtin_amdgcn_fmed3f(r[i], (float)LO, 127.0f);
+}
+
+__device__ __forceinline__ int8_t quantize_int8_fast(float x, float scale, float inv) {
+  const float xs[1] = {x};
+  int q[1];
+  quantize_int8_fast_n<1>(xs, scale, inv, q);
+  return (int8_t)q[0];
 }
 #endif
 

@@ -32,6 +32,8 @@ int8_linear = Op("int8_linear")
 mxfp8_linear = Op("mxfp8_linear", weights=1)
 mxfp8_scaled_mm = Op("mxfp8_scaled_mm")
 mxfp8_gelu_mlp = Op("mxfp8_gelu_mlp")
+conv2d_small_cin_quantize_int8 = Op("conv2d_small_cin_quantize_int8", composite=True, weights=2)
+bias_relu_quantize_int8 = Op("bias_relu_quantize_int8")
 # this backend's refiner-block producer (folded BatchNorm + GELU)
 depthwise5x5_gelu = Op("depthwise5x5_gelu")
 
@@ -60,7 +62,14 @@ IMPLS = (
     ("mxfp8_scaled_mm", _gemm.mxfp8_scaled_mm, (Feature.HIP, Feature.MFMA_F8F6F4_SCALED),
      _gemm.eligible_mxfp8_scaled_mm),
     ("mxfp8_gelu_mlp", _gemm.mxfp8_gelu_mlp, (Feature.HIP, Feature.MFMA_F8F6F4_SCALED), _gemm.eligible_mxfp8_gelu_mlp),
+    ("bias_relu_quantize_int8", _conv.bias_relu_quantize_int8, (Feature.HIP,), _conv.eligible_bias_relu_quantize),
 )
 
 for _name, _fn, _requires, _when in IMPLS:
     OPS[_name].register(HIP, device=ROCM, requires=_requires, priority=2, when=_when)(_fn)
+
+# the stem conv packs its weights once per bind (FlashIM's prepare / accepts, flashim/backends/triton/conv.py:925-950)
+conv2d_small_cin_quantize_int8.register(
+    HIP, device=ROCM, requires=(Feature.HIP,), priority=2, when=_conv.eligible_small_cin,
+    accepts=_conv.accepts_small_cin, prepare=_conv.small_cin_prepare,
+)(_conv.conv2d_small_cin_quantize_int8)

@@ -94,9 +94,22 @@ def _eligible_mxfp8_gelu_mlp(x, w1, b1, hidden_exponent, w2) -> bool:
     return _gemm.eligible_mxfp8_gelu_mlp(act, lw1, b1, hidden_exponent, lw2)
 
 
+def _adapt_stem(upstream_tensor_module):
+    def conv2d_small_cin_quantize_int8(x, scale, packed, bias):
+        q = _conv.conv2d_small_cin_quantize_int8(x, scale, packed, bias)
+        return upstream_tensor_module.Int8Tensor(q.values, q.scale)
+
+    def bias_relu_quantize_int8(raw, bias, scale):
+        q = _conv.bias_relu_quantize_int8(raw, bias, scale)
+        return upstream_tensor_module.Int8Tensor(q.values, q.scale)
+
+    return conv2d_small_cin_quantize_int8, bias_relu_quantize_int8
+
+
 def impls(upstream_tensor_module) -> dict[str, tuple[Callable, Callable]]:
     """``{op name: (impl, when)}`` for the FlashIM ops this backend replaces."""
     quantize_mxfp8, quantize_int8 = _adapt_quantized(upstream_tensor_module)
+    _, bias_relu_quantize_int8 = _adapt_stem(upstream_tensor_module)
     return {
         "quantize_mxfp8": (quantize_mxfp8, _quantize.eligible_quantize_mxfp8),
         "quantize_int8": (quantize_int8, _quantize.eligible_quantize_int8),
@@ -113,6 +126,16 @@ def impls(upstream_tensor_module) -> dict[str, tuple[Callable, Callable]]:
         "mxfp8_scaled_mm": (_gemm.mxfp8_scaled_mm, _gemm.eligible_mxfp8_scaled_mm),
         "mxfp8_linear": (_mxfp8_linear, _eligible_mxfp8_linear),
         "mxfp8_gelu_mlp": (_mxfp8_gelu_mlp, _eligible_mxfp8_gelu_mlp),
+        "bias_relu_quantize_int8": (bias_relu_quantize_int8, _conv.eligible_bias_relu_quantize),
+    }
+
+
+# ops whose impl packs its weights once per bind: {op name: (impl, when, accepts, prepare)}
+def prepared_impls(upstream_tensor_module) -> dict[str, tuple[Callable, Callable, Callable, Callable]]:
+    conv2d_small_cin_quantize_int8, _ = _adapt_stem(upstream_tensor_module)
+    return {
+        "conv2d_small_cin_quantize_int8": (conv2d_small_cin_quantize_int8, _conv.eligible_small_cin,
+                                           _conv.accepts_small_cin, _conv.small_cin_prepare),
     }
 
 
@@ -131,6 +154,15 @@ def register(flashim_ops=None, flashim_registry=None, flashim_tensor=None) -> li
         if any(impl.name == HIP for impl in getattr(op, "impls", [])):
             continue
         op.register(HIP, device=device, priority=PRIORITY, when=_guard(when))(fn)
+        done.append(name)
+    for name, (fn, when, accepts, prepare) in prepared_impls(flashim_tensor).items():
+        op = getattr(flashim_ops, name, None)
+        if op is None:
+            logger.info("FlashIM has no op %s; skipped", name)
+            continue
+        if any(impl.name == HIP for impl in getattr(op, "impls", [])):
+            continue
+        op.register(HIP, device=device, priority=PRIORITY, when=_guard(when), accepts=accepts, prepare=prepare)(fn)
         done.append(name)
     REGISTERED.extend(done)
     return done

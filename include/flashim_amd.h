@@ -129,6 +129,21 @@ int fim_refiner_mlp(int kind, int semantics, const uint8_t* x, int64_t P, int64_
                     const uint8_t* w2, const void* w2_scale, const void* b2, int b2_dtype, const uint16_t* residual,
                     uint16_t* out, hipStream_t stream);
 
+/* The first conv of a VGG encoder with its epilogue: quantize_int8(relu(bf16(conv3x3(x)) + bias)), stride 1,
+ * padding 1. x BF16 NCHW [B, Cin, H, W], Cin <= 8; w_packed BF16 [Cout, KP], KP = 32 ceil(9 Cin / 32), tap
+ * k = 9 c + 3 ky + kx (the [Cout, Cin, 3, 3] weight flattened) and zero beyond 9 Cin; Cout a power of two in
+ * [16, 128]; bias [Cout] (bias_dtype 1 BF16: the sum rounds to BF16; 0 FP32: it does not); scale FP32 scalar;
+ * out INT8 NHWC [B, H, W, Cout]. Replaces ops.conv2d_small_cin_quantize_int8 (flashim/ops/conv.py:225-235). */
+int fim_conv3x3_small_cin_quantize_int8(const uint16_t* x, int64_t B, int64_t Cin, int64_t H, int64_t W,
+                                        const uint16_t* w_packed, int64_t Cout, const void* bias, int bias_dtype,
+                                        const float* scale, int8_t* out, hipStream_t stream);
+
+/* quantize_int8(relu(raw + bias)) of a bias-free conv output: raw BF16 NCHW [B, C, H, W] -> INT8 NHWC [B, H, W, C];
+ * bias [C] BF16 (bias_dtype 1) or FP32 (0), scale FP32 scalar. Replaces ops.bias_relu_quantize_int8
+ * (flashim/ops/quantize.py:134-142). */
+int fim_bias_relu_quantize_int8(const uint16_t* raw, int64_t B, int64_t C, int64_t H, int64_t W, const void* bias,
+                                int bias_dtype, const float* scale, int8_t* out, hipStream_t stream);
+
 /* im2col of a 1-byte NHWC tensor: out [B*Ho*Wo, kh*kw*C] in (ky, kx, c) order with zero padding. Replaces
  * ops.im2col_gather (flashim/ops/conv.py:144-168). */
 int fim_im2col_gather(const uint8_t* x, int64_t B, int64_t H, int64_t W, int64_t C, int kh, int kw, int sh, int sw,

@@ -362,3 +362,19 @@ def depthwise5x5_relu_pointwise_int8(value: Tensor, dw_weight: Tensor, dw_bias: 
     quantized = depthwise5x5_relu_int8(value, dw_weight, dw_bias, scale)
     out = int8_linear(quantized, pw_weight, scale, pw_wscale, pw_bias)
     return out.reshape(batch, height, width, channels).permute(0, 3, 1, 2)
+
+
+# -- ops/quantize.py:134-142 and ops/conv.py:225-235: the VGG stem ------------------------------------------------
+
+
+def bias_relu_quantize_int8(raw: Tensor, bias: Tensor, scale: Tensor) -> Tensor:
+    """ops/quantize.py:134-142: ``quantize_int8_static(relu(raw + bias))`` of a bias-free NCHW conv output, the bias
+    added in the promoted dtype (BF16 + BF16 rounds to BF16, BF16 + FP32 stays FP32); int8 NHWC values."""
+    return quantize_int8_static(F.relu(raw + bias.view(1, -1, 1, 1)).permute(0, 2, 3, 1), scale)
+
+
+def conv2d_small_cin_quantize_int8(x: Tensor, scale: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
+    """ops/conv.py:225-235: the 3x3 / pad 1 conv of a small-Cin BF16 NCHW image rounded to BF16 (torch's BF16 conv:
+    FP32 accumulation, one rounding), then :func:`bias_relu_quantize_int8`; int8 NHWC values."""
+    return bias_relu_quantize_int8(F.conv2d(x, weight, None, padding=1), bias, scale)
+

@@ -216,6 +216,41 @@ def test_depthwise_oracle_against_float64():
     assert (z.float() == 0).all() and (zs[: 2 * 9 * 11 * 2] == 0).all()  # E8M0 0 = 2^-127
 
 
+# -- the VGG stem: bias_relu_quantize_int8 / conv2d_small_cin_quantize_int8 -------------------------------------
+
+
+def test_bias_relu_quantize_known_answers():
+    """Hand-derived codes: ReLU, torch's round-half-even, saturation; and the dtype promotion of the bias add
+    (ops/quantize.py:134-142): raw 1.0 + bias 2^-7 + 2^-10 is 1 + 2^-7 in BF16 (the 2^-10 is under half a BF16 step)
+    -> 64.5 steps of 1/64 -> code 64 (tie to even), but 1.0087890625 in FP32 -> 64.5625 -> code 65."""
+    raw = torch.tensor([-1.0, 0.0, 0.5, 1.5, 2.5, 200.0]).to(torch.bfloat16).view(1, 6, 1, 1)
+    got = ref.bias_relu_quantize_int8(raw, torch.zeros(6, dtype=torch.bfloat16), torch.tensor(1.0))
+    assert got.shape == (1, 1, 1, 6) and got.flatten().tolist() == [0, 0, 0, 2, 2, 127]
+    one = torch.ones(1, 1, 1, 1, dtype=torch.bfloat16)
+    b = 2.0**-7 + 2.0**-10
+    assert ref.bias_relu_quantize_int8(one, torch.tensor([b], dtype=torch.bfloat16), torch.tensor(1 / 64)).item() == 64
+    assert ref.bias_relu_quantize_int8(one, torch.tensor([b], dtype=torch.float32), torch.tensor(1 / 64)).item() == 65
+
+
+def test_small_cin_oracle_against_float64():
+    """torch's CPU BF16 conv is one BF16 rounding of the FP32-accumulated sum: against float64 of the same BF16
+    operands rounded once to BF16 it differs by at most one BF16 step on a tiny fraction (accumulation order), and the
+    INT8 codes by at most one step (FlashIM's own contract for this op, tests/ops/test_ops_cuda.py:543-555)."""
+    torch.manual_seed(12)
+    x = torch.randn(2, 3, 23, 37).to(torch.bfloat16)
+    w = (torch.randn(32, 3, 3, 3) * 0.3).to(torch.bfloat16)
+    bias = torch.randn(32).to(torch.bfloat16)
+    scale = torch.tensor(0.04)
+    conv = F.conv2d(x, w, None, padding=1)
+    exact = F.conv2d(x.double(), w.double(), None, padding=1).to(torch.bfloat16)
+    step = exact.float().abs().clamp_min(2.0**-126) * 2.0**-7
+    assert ((conv.float() - exact.float()).abs() <= step).all() and (conv != exact).float().mean() < 1e-3
+    got = ref.conv2d_small_cin_quantize_int8(x, scale, w, bias)
+    want = ((F.relu(exact + bias.view(1, -1, 1, 1)).float() / 0.04).round().clamp(-127, 127)).permute(0, 2, 3, 1)
+    assert got.shape == (2, 23, 37, 32) and got.dtype == torch.int8
+    assert (got.float() - want).abs().max() <= 1 and (got.float() != want).float().mean() < 1e-3
+
+
 # -- golden fixtures ---------------------------------------------------------------------------------------------
 
 

@@ -15,9 +15,12 @@ def _stub_flashim():
     for name in ("quantize_mxfp8", "quantize_int8", "int8_conv2d", "mxfp8_conv2d", "depthwise5x5_relu_mxfp8",
                  "depthwise5x5_relu_int8", "depthwise5x5_relu_pointwise_mxfp8", "depthwise5x5_relu_pointwise_int8",
                  "im2col_gather", "int8_conv2d_maxpool", "int8_linear", "mxfp8_scaled_mm", "mxfp8_linear",
-                 "mxfp8_gelu_mlp"):
+                 "mxfp8_gelu_mlp", "bias_relu_quantize_int8"):
         registry.OPS.pop("stub_" + name, None)
         setattr(ops, name, registry.Op("stub_" + name, lambda *a, **k: "reference"))
+    registry.OPS.pop("stub_conv2d_small_cin_quantize_int8", None)
+    ops.conv2d_small_cin_quantize_int8 = registry.Op("stub_conv2d_small_cin_quantize_int8", lambda *a, **k: "reference",
+                                                     composite=True, weights=2)
 
     @dataclass(frozen=True)
     class QuantizedTensor:
@@ -40,7 +43,7 @@ def test_plugin_registers_hip_impls_for_rocm():
     assert set(done) == {"quantize_mxfp8", "quantize_int8", "int8_conv2d", "mxfp8_conv2d",
                          "depthwise5x5_relu_mxfp8", "depthwise5x5_relu_int8", "depthwise5x5_relu_pointwise_mxfp8",
                          "depthwise5x5_relu_pointwise_int8", "im2col_gather", "int8_conv2d_maxpool", "int8_linear", "mxfp8_scaled_mm",
-                         "mxfp8_linear", "mxfp8_gelu_mlp"}
+                         "mxfp8_linear", "mxfp8_gelu_mlp", "bias_relu_quantize_int8", "conv2d_small_cin_quantize_int8"}
     for name in done:
         impl = getattr(ops, name).impls[-1]
         assert impl.name == "hip" and impl.device == reg.DeviceSpec("rocm") and impl.priority == plugin.PRIORITY
