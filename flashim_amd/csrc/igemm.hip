@@ -57,6 +57,7 @@ struct ConvArgs {
   int kh, kw, sh, sw, ph, pw, dh, dw;
   int M;                   // output pixels (< 2^31)
   int kchunks;             // ceil(Cin / 128)
+  int tps;                 // taps per 128-byte K step of the packed-tap kernels (PACK): 128 / Cin for Cin 16, 32, 64
   int n_tiles, m_tiles;
   int m_base;              // first GEMM row of this launch (a split launch runs its last rows as a second launch)
 };
@@ -396,7 +397,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc
   }
 }
 
-template <int KIND, int BN, int LW, int OUT, int XS, int POOL, int MBW = 4>
+template <int KIND, int BN, int LW, int OUT, int XS, int POOL, int MBW = 4, bool PACK = false>
 __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
   constexpr int MB = MBW;                // 16-pixel blocks per wavefront (64 pixels; 32 in the tail's small tiles)
   constexpr int BM = 32 * MB;            // pixel rows per tile: two wavefronts of MB blocks
@@ -509,22 +510,43 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
 
   // (tap, channel chunk) of the step being loaded; advanced uniformly
   int ld_ky = 0, ld_kx = 0, ld_c0 = 0;
+  int ld_tap0 = 0;  // packed taps (tps > 1): the step's first tap
+  const int taps_total = a.kh * a.kw;
+  const int seg_sub = (seg * 16) / a.Cin, seg_coff = (seg * 16) % a.Cin;  // packed: this segment's tap and channel
   auto gload = [&](uint4 (&ra)[A_PASSES], uint4 (&rb)[B_PASSES], int (&pre_sx)[SXN], int (&pre_sw)[NB], bool& pre_ok) {
-    const int dy = ld_ky * a.dh, dx = ld_kx * a.dw;
-    const int64_t delta = (int64_t)(dy * a.W + dx) * a.Cin + ld_c0;
-    const int cvalid = a.Cin - ld_c0 - seg * 16;
+    int dy, dx, cvalid;
+    int64_t delta, wdelta;
+    if constexpr (PACK) {
+      // several taps per step: segment seg holds channels [seg_coff, + 16) of tap ld_tap0 + seg_sub (taps past the
+      // filter load the zero segment); the weights of consecutive taps are contiguous in a weight row
+      const int tap = ld_tap0 + seg_sub;
+      const bool tap_ok = tap < taps_total;
+      const int ky = tap_ok ? tap / a.kw : 0, kx = tap_ok ? tap - ky * a.kw : 0;
+      dy = ky * a.dh;
+      dx = kx * a.dw;
+      delta = (int64_t)(dy * a.W + dx) * a.Cin + seg_coff - seg * 16;
+      cvalid = tap_ok ? 16 : 0;
+      wdelta = (int64_t)ld_tap0 * a.Cin;
+    } else {
+      dy = ld_ky * a.dh;
+      dx = ld_kx * a.dw;
+      delta = (int64_t)(dy * a.W + dx) * a.Cin + ld_c0;
+      cvalid = a.Cin - ld_c0 - seg * 16;
+      wdelta = (int64_t)(ld_ky * a.kw + ld_kx) * a.Cin + ld_c0;
+    }
 #pragma unroll
     for (int j = 0; j < A_PASSES; ++j) {
       const bool ok = (unsigned)(a_h[j] + dy) < (unsigned)a.H && (unsigned)(a_w[j] + dx) < (unsigned)a.W;
       ra[j] = load_seg<LW>(a_ptr[j] + delta, ok, cvalid);
     }
-    const int64_t wdelta = (int64_t)(ld_ky * a.kw + ld_kx) * a.Cin + ld_c0;
 #pragma unroll
     for (int j = 0; j < B_PASSES; ++j) rb[j] = load_seg<LW>(b_ptr[j] + wdelta, b_ok[j], cvalid);
     if (KIND == KIND_MX) {
       // raw exponent bytes, loaded unconditionally from clamped indices and only turned into E8M0 when the step is
       // computed: consuming them here would make the compiler wait for every load issued so far
-      const int blk = (ld_c0 >> 5) + g;
+      // K block g of the step: packed taps take tap ld_tap0 + 32 g / Cin, channel block (32 g % Cin) / 32
+      const int ptap = ld_tap0 + (32 * g) / a.Cin;
+      const int blk = PACK ? ((32 * g) % a.Cin) >> 5 : (ld_c0 >> 5) + g;
       const int cblk = blk < cblocks ? blk : cblocks - 1;
       if (XS == 0) {
         pre_sx[0] = (int)a.x_expo[cblk];
@@ -538,11 +560,12 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
                                    (rt >> 5) * 4 + (cblk & 3)];
         }
       }
-      pre_ok = blk < cblocks;
-      const int wblk = (ld_ky * a.kw + ld_kx) * cblocks + cblk;
+      pre_ok = PACK ? ptap < taps_total : blk < cblocks;
+      const int wblk = PACK ? min(ptap, taps_total - 1) * cblocks + cblk : (ld_ky * a.kw + ld_kx) * cblocks + cblk;
 #pragma unroll
       for (int i = 0; i < NB; ++i) pre_sw[i] = (int)wexp_row[i][wblk];
     }
+    ld_tap0 += a.tps;
     ld_c0 += KC;
     if (ld_c0 >= a.Cin) {
       ld_c0 = 0;
@@ -570,7 +593,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
       acc_f[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
     }
 
-  const int nk = a.kh * a.kw * a.kchunks;
+  const int nk = PACK ? (a.kh * a.kw + a.tps - 1) / a.tps : a.kh * a.kw * a.kchunks;
   gload(ra0, rb0, sx0, sw0, bok0);
   if (nk > 1) gload(ra1, rb1, sx1, sw1, bok1);
   sstore(0, ra0, rb0);
@@ -671,17 +694,23 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
 }
 
 
-// The tail of a split launch: 64 x 64 tiles (2 x 2 blocks per wavefront) on the plain path.
+// 64 x 64 tiles (2 x 2 blocks per wavefront) on the plain path: the tail of a split launch, and launches too small to
+// reach every CU with 128-row tiles. With a.tps > 1 (Cin 16, 32, 64; 16-byte loads) the packed-tap variant.
 template <int KIND>
 static void launch_tail(const ConvArgs& a, int lw, dim3 grid, hipStream_t stream) {
   constexpr int QOUT = KIND == KIND_INT8 ? OUT_INT8 : OUT_E4M3;
+  const bool pack = a.tps > 1 && lw == 16;
   if (a.out_mode == OUT_BF16) {
-    if (lw == 16)
+    if (pack)
+      conv_igemm_kernel<KIND, 64, 16, OUT_BF16, 0, 0, 2, true><<<grid, dim3(256), 0, stream>>>(a);
+    else if (lw == 16)
       conv_igemm_kernel<KIND, 64, 16, OUT_BF16, 0, 0, 2><<<grid, dim3(256), 0, stream>>>(a);
     else
       conv_igemm_kernel<KIND, 64, 1, OUT_BF16, 0, 0, 2><<<grid, dim3(256), 0, stream>>>(a);
   } else {
-    if (lw == 16)
+    if (pack)
+      conv_igemm_kernel<KIND, 64, 16, QOUT, 0, 0, 2, true><<<grid, dim3(256), 0, stream>>>(a);
+    else if (lw == 16)
       conv_igemm_kernel<KIND, 64, 16, QOUT, 0, 0, 2><<<grid, dim3(256), 0, stream>>>(a);
     else
       conv_igemm_kernel<KIND, 64, 1, QOUT, 0, 0, 2><<<grid, dim3(256), 0, stream>>>(a);
@@ -739,9 +768,14 @@ static int launch_conv(ConvArgs a, hipStream_t stream) {
     return FIM_ERR_UNSUPPORTED;
   a.M = (int)M;
   a.kchunks = (a.Cin + KC - 1) / KC;
+  a.tps = 1;
   int lw = 1;
   const uintptr_t both = (uintptr_t)a.x | (uintptr_t)a.w;
   if (a.Cin % 16 == 0 && both % 16 == 0) lw = 16;
+  // Cin 16, 32 or 64: the 64 x 64-tile kernels pack 128 / Cin taps into each 128-byte K step instead of padding every
+  // step with zeros (MXFP8 needs whole 32-channel scale blocks)
+  if (lw == 16 && a.kh * a.kw > 1 && (a.Cin == 64 || a.Cin == 32 || (a.Cin == 16 && KIND == KIND_INT8)))
+    a.tps = KC / a.Cin;
   const int bn = (a.Cout > 64 && a.x_swz == nullptr) ? 128 : 64;
   a.n_tiles = (a.Cout + bn - 1) / bn;
   const int64_t m_tiles = (a.M + BM_MAIN - 1) / BM_MAIN;
@@ -754,6 +788,17 @@ static int launch_conv(ConvArgs a, hipStream_t stream) {
   // complete rounds run as one launch and the remaining rows as a second launch of 64 x 64 tiles (4x as many, each
   // about a quarter of the work), which fills the last round instead.
   if (a.x_swz == nullptr && a.pool_out == nullptr) {
+#ifndef FIM_EXP_NO_SMALL
+    // fewer 128-row tiles than CUs: 64 x 64 tiles instead, so the launch reaches every CU (e.g. config 1: 128 tiles
+    // of 128 x 64 -> 256 of 64 x 64)
+    if (tiles < device_cus()) {
+      ConvArgs t = a;
+      t.n_tiles = (a.Cout + 63) / 64;
+      t.m_tiles = (int)cdiv(a.M, 64);
+      launch_tail<KIND>(t, lw, dim3((unsigned)(cdiv((int64_t)t.m_tiles * t.n_tiles, 8) * 8)), stream);
+      return launch_status();
+    }
+#endif
     const int64_t slots = 2LL * device_cus();
     const int64_t full = tiles / slots, rem = tiles - full * slots;
     const int64_t mt_main = full * slots / a.n_tiles;
