@@ -11,7 +11,7 @@
 // Layout: input BF16 NHWC [B, H, W, C] (the channels-last memory of [B, C, H, W]); weight BF16 [25, C] (ky, kx major,
 // flashim/quant/passes/separable_conv_block.py:52-55); bias FP32 [C]. Output row = pixel (b, y, x), C channels.
 //
-// Work split: see the tile comment at dw5x5_kernel. The weights of a lane's 4 channels live in VGPRs as 60 BF16 pairs.
+// Work split: see the tile and matrix-unit comments below (dw5x5_mfma_kernel).
 #include <type_traits>
 
 #include "common.h"
@@ -20,14 +20,6 @@ namespace fim {
 
 enum { ACT_RELU = 0, ACT_GELU = 1 };
 enum { DW_MX_DYNAMIC = 0, DW_INT8 = 1, DW_BF16 = 2, DW_MX_STATIC = 3 };
-
-__device__ __forceinline__ void load4_bf16(const uint16_t* p, float* v) {
-  uint2 q = *reinterpret_cast<const uint2*>(p);
-  v[0] = u2f(q.x << 16);
-  v[1] = u2f(q.x & 0xffff0000u);
-  v[2] = u2f(q.y << 16);
-  v[3] = u2f(q.y & 0xffff0000u);
-}
 
 struct DwArgs {
   const uint16_t* x;
@@ -41,209 +33,239 @@ struct DwArgs {
   int B, H, W, C;
 };
 
-// Tile: 32 output columns x 16 output rows x 32 channels per workgroup. The (16 + 4) x (32 + 4) input pixels of the
-// 32-channel slice are staged in LDS once, with adjacent columns interleaved per channel: dword (row, column pair p,
-// channel c) holds the BF16 values of columns 2p and 2p + 1, so two horizontal taps of one channel are one
-// v_dot2_f32_bf16 operand (two products, FP32 accumulate). A lane owns 4 channels of one output column x and covers its
-// 5 taps of a row with 3 dot2 steps: columns (x, x+1), (x+2, x+3), (x+4, x+5) with weight pairs (w0, w1), (w2, w3),
-// (w4, 0) when x is even; (x-1, x), (x+1, x+2), (x+3, x+4) with (0, w0), (w1, w2), (w3, w4) when x is odd. The lane
-// walks the 20 input rows; row s feeds output rows s - ky for the 5 ky, held in a ring of 5 accumulators indexed at
-// compile time (the row loop is unrolled by 5), and output row s - 4 is complete after row s. The FP32 sums are those
-// of a direct 25-tap loop in another order (per ky: the dot2 pairs, then the rows).
+// Tile: 32 output columns x 16 output rows x 32 channels per workgroup (grid: column tiles, row tiles, batch x
+// 32-channel slices), with the 2-pixel halo of the 5x5 window staged in LDS once.
 constexpr int DW_TW = 32, DW_TH = 16, DW_CS = 32;  // output columns, output rows, channels per workgroup
-constexpr int DW_IW = DW_TW + 4, DW_IH = DW_TH + 4;
-constexpr int DW_PAIRS = DW_IW / 2;                // 18 column pairs per staged row
 
-typedef __bf16 v2bf16 __attribute__((ext_vector_type(2)));
+// ---- The taps on the matrix unit ----------------------------------------------------------------------------
+// v_mfma_f32_4x4x4_16b_bf16 runs 16 independent 4x4x4 products per instruction; each is one channel: D[i][j] (output
+// columns 4 cq + i, output row 4 rq + j) += A[i][k] B[k][j] with A the Toeplitz matrix of one weight row, A[i][k] =
+// w[ky][4 s + k - i] (zero outside 0..4), and B[k][j] = input (row 4 rq + j + ky, column 4 cq + 4 s + k) of the staged
+// tile (origin y0 - 2, x0 - 2): 5 weight rows x 2 column segments s = 10 MFMAs per 16 channels x 4 x 4 outputs.
+// Operand layout (measured): lane l = 4 b + r supplies A_b[r][0..3] and B_b[0..3][r] and gets D_b[0..3][r].
+// The tile is staged channel-planar ([channel][row][column] BF16, 40 columns per row, planes 402 dwords apart so the
+// 16 channels of an instruction fall on different banks) so each B operand is one 8-byte LDS read. After the taps the
+// activated FP32 values go through LDS in two 8-row halves ([row][column][channel], rows padded by 16 dwords) and the
+// output pass writes per pixel: 8 channels per lane, MX dynamic exponents from 4-lane amax shuffles.
+constexpr int DWM_ROWSTR = 20;                      // dwords per staged row (40 columns, 36 used)
+constexpr int DWM_PLANE = 20 * DWM_ROWSTR + 2;      // dwords per channel plane
+constexpr int DWM_LDS = DW_CS * DWM_PLANE;          // 12864 dwords
+constexpr int DWM_OROW = DW_TW * DW_CS + 16;        // dwords per staged output row (FP32, padded)
+static_assert(8 * DWM_OROW <= DWM_LDS, "an 8-row output half fits in the input tile's space");
 
-__device__ __forceinline__ v2bf16 as_bf2(uint32_t u) { return __builtin_bit_cast(v2bf16, u); }
+typedef __bf16 v4bf16 __attribute__((ext_vector_type(4)));
 
 template <int ACT, int OUT>
-__global__ __launch_bounds__(256) void dw5x5_kernel(const DwArgs a) {
-  __shared__ __attribute__((aligned(16))) uint32_t tile[DW_IH * DW_PAIRS * DW_CS];  // [row][pair][32 ch], 46 KB
-  const int tid = threadIdx.x;
+__global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
+  __shared__ __attribute__((aligned(16))) uint32_t sm[DWM_LDS];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int x0 = blockIdx.x * DW_TW;
   const int y0 = blockIdx.y * DW_TH;
   const int cslices = a.C / DW_CS;
   const int b = blockIdx.z / cslices;
   const int cbase = (blockIdx.z % cslices) * DW_CS;
 
-  // stage: 20 rows x 18 column pairs x 4 segments of 8 channels; each item loads the 8 channels of both columns
-  // (zero outside the image) and interleaves them (v_perm) into 8 dwords
-  for (int i = tid; i < DW_IH * DW_PAIRS * 4; i += 256) {
-    const int segi = i & 3, rp = i >> 2;
-    const int r = rp / DW_PAIRS, p = rp - r * DW_PAIRS;
-    const int iy = y0 - 2 + r, ix = x0 - 2 + 2 * p;
-    uint4 va = make_uint4(0, 0, 0, 0), vb = make_uint4(0, 0, 0, 0);
+  // stage: unit (row r, 4-column group q, channel octet o): 4 pixels x 8 channels, transposed (v_perm) into 8
+  // channel rows of 4 BF16, one 8-byte LDS write each; loads unconditional from clamped in-image addresses
+  for (int u = tid; u < 20 * 10 * 4; u += 256) {
+    const int o = u & 3, rq = u >> 2;
+    const int r = rq / 10, q = rq - r * 10;
+    const int iy = y0 - 2 + r;
     const bool row_ok = iy >= 0 && iy < a.H;
-    const uint16_t* src = a.x + (((int64_t)b * a.H + (row_ok ? iy : 0)) * a.W) * a.C + cbase + segi * 8;
-    if (row_ok && ix >= 0 && ix < a.W) va = *reinterpret_cast<const uint4*>(src + (int64_t)ix * a.C);
-    if (row_ok && ix + 1 >= 0 && ix + 1 < a.W) vb = *reinterpret_cast<const uint4*>(src + (int64_t)(ix + 1) * a.C);
-    const uint32_t A[4] = {va.x, va.y, va.z, va.w}, B[4] = {vb.x, vb.y, vb.z, vb.w};
-    uint32_t o[8];
+    const uint16_t* src_row = a.x + ((int64_t)b * a.H + min(max(iy, 0), a.H - 1)) * a.W * a.C + cbase + 8 * o;
+    uint32_t P[4][4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      o[2 * k] = __builtin_amdgcn_perm(B[k], A[k], 0x05040100u);      // channel 2k: (col 2p, col 2p + 1)
-      o[2 * k + 1] = __builtin_amdgcn_perm(B[k], A[k], 0x07060302u);  // channel 2k + 1
+      const int ix = x0 - 2 + 4 * q + k;
+      const bool ok = row_ok && ix >= 0 && ix < a.W;
+      const uint4 v = *reinterpret_cast<const uint4*>(src_row + (int64_t)min(max(ix, 0), a.W - 1) * a.C);
+      P[k][0] = ok ? v.x : 0u; P[k][1] = ok ? v.y : 0u; P[k][2] = ok ? v.z : 0u; P[k][3] = ok ? v.w : 0u;
     }
-    uint32_t* dst = &tile[(r * DW_PAIRS + p) * DW_CS + segi * 8];
-    *reinterpret_cast<uint4*>(dst) = make_uint4(o[0], o[1], o[2], o[3]);
-    *reinterpret_cast<uint4*>(dst + 4) = make_uint4(o[4], o[5], o[6], o[7]);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {  // dword m of a pixel = channels 8 o + 2 m (low half), + 1 (high half)
+      const uint32_t lo01 = __builtin_amdgcn_perm(P[1][m], P[0][m], 0x05040100u);
+      const uint32_t lo23 = __builtin_amdgcn_perm(P[3][m], P[2][m], 0x05040100u);
+      const uint32_t hi01 = __builtin_amdgcn_perm(P[1][m], P[0][m], 0x07060302u);
+      const uint32_t hi23 = __builtin_amdgcn_perm(P[3][m], P[2][m], 0x07060302u);
+      const int c0 = 8 * o + 2 * m;
+      *reinterpret_cast<uint2*>(&sm[c0 * DWM_PLANE + r * DWM_ROWSTR + 2 * q]) = make_uint2(lo01, lo23);
+      *reinterpret_cast<uint2*>(&sm[(c0 + 1) * DWM_PLANE + r * DWM_ROWSTR + 2 * q]) = make_uint2(hi01, hi23);
+    }
   }
 
-  const int lane = tid & 63, wave = tid >> 6;
-  const int cq = lane & 7;                   // channel quad within the 32-channel slice
-  const int xl = wave * 8 + (lane >> 3);     // output column within the tile
-  const int x = x0 + xl;
-  const int c = cbase + cq * 4;
-  const bool x_ok = x < a.W;
-  const bool odd = (xl & 1) != 0;
-  const int pb = xl >> 1;                    // first column pair of this lane's taps
-
-  // weight pairs per (ky, dot2 step k, channel): (w[ky][2k], w[ky][2k+1]) for even columns, shifted by one for odd
-  uint32_t wp[5][3][4];
+  // this lane's channel (block b of the wave's 16-channel group) and row/column index r4 within the 4 x 4 blocks
+  const int cg = wave & 1, rh = wave >> 1;  // channel group; row half (row quads 2 rh, 2 rh + 1)
+  const int bch = lane >> 2, r4 = lane & 3;
+  const int ch = cbase + 16 * cg + bch;
+  // A operands: row r4 of the Toeplitz matrix of weight row ky, column segment s. With v = (w0, w1, w2, w3) and
+  // u = (w1, w2, w3, w4) as 64-bit vectors of BF16 (element k in bits 16 k), segment 0 is v shifted up by r4 elements
+  // (zeros enter below) and segment 1 is u shifted down by 3 - r4 elements.
+  v4bf16 wa[5][2];
 #pragma unroll
   for (int ky = 0; ky < 5; ++ky) {
-    uint32_t w5[5][4];  // BF16 bits of w[ky][kx] for the lane's 4 channels
+    uint64_t w5[5];
 #pragma unroll
-    for (int kx = 0; kx < 5; ++kx) {
-      const uint2 q = *reinterpret_cast<const uint2*>(a.w + (ky * 5 + kx) * a.C + c);
-      w5[kx][0] = q.x & 0xffffu; w5[kx][1] = q.x >> 16; w5[kx][2] = q.y & 0xffffu; w5[kx][3] = q.y >> 16;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t e0 = w5[0][i] | (w5[1][i] << 16), e1 = w5[2][i] | (w5[3][i] << 16), e2 = w5[4][i];
-      const uint32_t o0 = w5[0][i] << 16, o1 = w5[1][i] | (w5[2][i] << 16), o2 = w5[3][i] | (w5[4][i] << 16);
-      wp[ky][0][i] = odd ? o0 : e0;
-      wp[ky][1][i] = odd ? o1 : e1;
-      wp[ky][2][i] = odd ? o2 : e2;
-    }
+    for (int kx = 0; kx < 5; ++kx) w5[kx] = a.w[(ky * 5 + kx) * a.C + ch];
+    const uint64_t v = w5[0] | (w5[1] << 16) | (w5[2] << 32) | (w5[3] << 48);
+    const uint64_t u = w5[1] | (w5[2] << 16) | (w5[3] << 32) | (w5[4] << 48);
+    wa[ky][0] = __builtin_bit_cast(v4bf16, v << (16 * r4));
+    wa[ky][1] = __builtin_bit_cast(v4bf16, u >> (16 * (3 - r4)));
   }
-  float bias[4];
+  const float bias = a.bias[ch];
+  __syncthreads();
+
+  v4f acc[2][8];  // [row quad 2 rh + t][column quad cq]: D[i = 0..3][j = r4]
 #pragma unroll
-  for (int i = 0; i < 4; ++i) bias[i] = a.bias[c + i];
-  float oscale = 0.f, oinv = 1.f;
-  float oinv8 = 1.f;
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int cq = 0; cq < 8; ++cq) acc[t][cq] = v4f{0.f, 0.f, 0.f, 0.f};
+  const uint32_t* plane = &sm[(16 * cg + bch) * DWM_PLANE];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int ky = 0; ky < 5; ++ky) {
+      const uint32_t* rowp = plane + (4 * (2 * rh + t) + r4 + ky) * DWM_ROWSTR;
+#pragma unroll
+      for (int cq = 0; cq < 8; ++cq)
+#pragma unroll
+        for (int sg = 0; sg < 2; ++sg) {
+          const uint2 raw = *reinterpret_cast<const uint2*>(rowp + 2 * cq + 2 * sg);
+          acc[t][cq] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(wa[ky][sg], __builtin_bit_cast(v4bf16, raw), acc[t][cq],
+                                                              0, 0, 0);
+        }
+    }
+
+  // activation in registers (bias; ReLU, or BF16 rounding + GELU + rounding), for all 64 values of the lane
+  float y[2][8][4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int cq = 0; cq < 8; ++cq)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[t][cq][i] = acc[t][cq][i] + bias;
+  if (ACT == ACT_RELU) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int cq = 0; cq < 8; ++cq)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[t][cq][i] = fmaxf(y[t][cq][i], 0.f);
+  } else {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int cq = 0; cq < 8; ++cq) {
+        float* v = y[t][cq];
+        round_bf16x2(v[0], v[1]);
+        round_bf16x2(v[2], v[3]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = gelu_erf(v[i]);
+        round_bf16x2(v[0], v[1]);
+        round_bf16x2(v[2], v[3]);
+      }
+  }
+
+  float oscale = 0.f, oinv8 = 1.f, oinv = 1.f;
   if (OUT == DW_INT8) {
     oscale = *a.scale;
     oinv8 = __fdiv_rn(1.0f, oscale);
   }
-  if (OUT == DW_MX_STATIC) oinv = exp2_int(-(int)a.expo[c >> 5]);
+  if (OUT == DW_MX_STATIC) oinv = exp2_int(-(int)a.expo[cbase >> 5]);
   const int64_t groups = a.C >> 5;
   const int64_t tiles_k = (groups + 3) >> 2;
-
-  __syncthreads();
-
-  float acc[5][4];  // ring: output row o accumulates in acc[o % 5]
+  const int rows = min(DW_TH, a.H - y0), cols = min(DW_TW, a.W - x0);
+  float* st = reinterpret_cast<float*>(sm);
 #pragma unroll
-  for (int k = 0; k < 5; ++k)
+  for (int half = 0; half < 2; ++half) {
+    __syncthreads();  // half 0: the taps are done with the input tile; half 1: the previous output pass is done
+    if (rh == half) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[k][i] = 0.f;
-
-  auto finish = [&](int oy, float (&sum)[4]) {
-    float y[4];
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) y[i] = sum[i] + bias[i];
-    if (ACT == ACT_RELU) {
+        for (int cq = 0; cq < 8; ++cq)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) y[i] = fmaxf(y[i], 0.f);
-    } else {
-      round_bf16x2(y[0], y[1]);
-      round_bf16x2(y[2], y[3]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) y[i] = gelu_erf(y[i]);
-      round_bf16x2(y[0], y[1]);
-      round_bf16x2(y[2], y[3]);
+          for (int i = 0; i < 4; ++i)
+            st[(4 * t + r4) * DWM_OROW + (4 * cq + i) * DW_CS + 16 * cg + bch] = y[t][cq][i];
     }
-    const int64_t row = ((int64_t)b * a.H + oy) * a.W + x;
-    if (OUT == DW_MX_DYNAMIC) {
-      float amax = fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3])));
-      amax = fmaxf(amax, __shfl_xor(amax, 1));
-      amax = fmaxf(amax, __shfl_xor(amax, 2));
-      amax = fmaxf(amax, __shfl_xor(amax, 4));
-      const int e = mx_exponent_from_amax(amax);
-      const float inv = exp2_int(-e);
-      if (x_ok) {
-        const uint32_t q = pack_e4m3x4(mx_scale_clamp(y[0], inv), mx_scale_clamp(y[1], inv),
-                                       mx_scale_clamp(y[2], inv), mx_scale_clamp(y[3], inv));
-        *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.out) + row * a.C + c) = q;
-        if (cq == 0) {
-          const int64_t gi = c >> 5;
-          if (a.expo_out != nullptr) a.expo_out[row * groups + gi] = (int8_t)e;
-          if (a.swizzled != nullptr) {
-            const int64_t rt = row & 127;
-            a.swizzled[(((row >> 7) * tiles_k + (gi >> 2)) << 9) + (rt & 31) * 16 + (rt >> 5) * 4 + (gi & 3)] =
-                (uint8_t)(e + 127);
+    __syncthreads();
+    // output pass: 8 rows x 32 columns x 4 parts of 8 channels; 4 consecutive lanes share a pixel
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int unit = tid + 256 * it;
+      const int part = unit & 3, px = unit >> 2;  // px: 8 rows x 32 columns
+      const int rl = px >> 5, col = px & 31;
+      const int oy = 8 * half + rl;
+      const float4 va = *reinterpret_cast<const float4*>(&st[rl * DWM_OROW + col * DW_CS + 8 * part]);
+      const float4 vb = *reinterpret_cast<const float4*>(&st[rl * DWM_OROW + col * DW_CS + 8 * part + 4]);
+      float v[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+      const bool ok = oy < rows && col < cols;
+      const int64_t row = ((int64_t)b * a.H + y0 + oy) * a.W + x0 + col;
+      const int c = cbase + 8 * part;
+      if (OUT == DW_MX_DYNAMIC) {
+        float amax = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+        amax = fmaxf(amax, __shfl_xor(amax, 1));
+        amax = fmaxf(amax, __shfl_xor(amax, 2));
+        const int ex = mx_exponent_from_amax(amax);
+        const float inv = exp2_int(-ex);
+        if (ok) {
+          *reinterpret_cast<uint2*>(static_cast<uint8_t*>(a.out) + row * a.C + c) =
+              make_uint2(pack_e4m3x4(mx_scale_clamp(v[0], inv), mx_scale_clamp(v[1], inv), mx_scale_clamp(v[2], inv),
+                                     mx_scale_clamp(v[3], inv)),
+                         pack_e4m3x4(mx_scale_clamp(v[4], inv), mx_scale_clamp(v[5], inv), mx_scale_clamp(v[6], inv),
+                                     mx_scale_clamp(v[7], inv)));
+          if (part == 0) {
+            const int64_t gi = cbase >> 5;
+            if (a.expo_out != nullptr) a.expo_out[row * groups + gi] = (int8_t)ex;
+            if (a.swizzled != nullptr) {
+              const int64_t rt = row & 127;
+              a.swizzled[(((row >> 7) * tiles_k + (gi >> 2)) << 9) + (rt & 31) * 16 + (rt >> 5) * 4 + (gi & 3)] =
+                  (uint8_t)(ex + 127);
+            }
           }
         }
-      }
-    } else if (x_ok) {
-      if (OUT == DW_INT8) {
+      } else if (OUT == DW_INT8) {
         if (ACT == ACT_RELU) {
-          round_bf16x2(y[0], y[1]);
-          round_bf16x2(y[2], y[3]);
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) round_bf16x2(v[e], v[e + 1]);
         }
-        int qi[4];
-        quantize_int8_fast_n<4>(y, oscale, oinv8, qi);
-        uint32_t q = 0;
+        int qi[8];
+        quantize_int8_fast_n<8>(v, oscale, oinv8, qi);
+        if (ok) {
+          uint32_t q0 = 0, q1 = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) q |= (uint32_t)(uint8_t)qi[i] << (8 * i);
-        *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.out) + row * a.C + c) = q;
+          for (int e = 0; e < 4; ++e) {
+            q0 |= (uint32_t)(uint8_t)qi[e] << (8 * e);
+            q1 |= (uint32_t)(uint8_t)qi[4 + e] << (8 * e);
+          }
+          *reinterpret_cast<uint2*>(static_cast<uint8_t*>(a.out) + row * a.C + c) = make_uint2(q0, q1);
+        }
       } else if (OUT == DW_MX_STATIC) {
-        const uint32_t q = pack_e4m3x4(mx_scale_clamp(y[0], oinv), mx_scale_clamp(y[1], oinv),
-                                       mx_scale_clamp(y[2], oinv), mx_scale_clamp(y[3], oinv));
-        *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.out) + row * a.C + c) = q;
+        if (ok)
+          *reinterpret_cast<uint2*>(static_cast<uint8_t*>(a.out) + row * a.C + c) =
+              make_uint2(pack_e4m3x4(mx_scale_clamp(v[0], oinv), mx_scale_clamp(v[1], oinv),
+                                     mx_scale_clamp(v[2], oinv), mx_scale_clamp(v[3], oinv)),
+                         pack_e4m3x4(mx_scale_clamp(v[4], oinv), mx_scale_clamp(v[5], oinv),
+                                     mx_scale_clamp(v[6], oinv), mx_scale_clamp(v[7], oinv)));
       } else {
-        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + row * a.C + c) =
-            make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+        if (ok)
+          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + row * a.C + c) =
+              make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                         pack_bf16x2(v[6], v[7]));
       }
     }
-  };
-
-  // one input row s (u = s mod 5, compile time): 3 pair reads, 60 dot2 into the ring, then output row s - 4
-  const int rows = min(DW_TH, a.H - y0);  // output rows of this tile
-  auto row_step = [&](int s, auto uc) {
-    constexpr int U = decltype(uc)::value;
-    const uint32_t* rp = &tile[(s * DW_PAIRS + pb) * DW_CS + cq * 4];
-    uint4 v[3];
-#pragma unroll
-    for (int k = 0; k < 3; ++k) v[k] = *reinterpret_cast<const uint4*>(rp + k * DW_CS);
-#pragma unroll
-    for (int ky = 0; ky < 5; ++ky) {
-      float* r = acc[(U - ky + 5) % 5];
-#pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        const uint32_t xv[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) r[i] = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(xv[i]), as_bf2(wp[ky][k][i]), r[i], false);
-      }
-    }
-    // row s - 4 (ring slot (U + 1) % 5) has all its taps: emit it (rows above the tile, s < 4, only collected the
-    // taps of the zero padding), then clear the slot for row s + 1
-    float* o = acc[(U + 1) % 5];
-    if (s >= 4) {
-      float sum[4] = {o[0], o[1], o[2], o[3]};
-      finish(y0 + s - 4, sum);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = 0.f;
-  };
-  for (int s = 0; s < rows + 4; s += 5) {
-    row_step(s, std::integral_constant<int, 0>{});
-    if (s + 1 < rows + 4) row_step(s + 1, std::integral_constant<int, 1>{});
-    if (s + 2 < rows + 4) row_step(s + 2, std::integral_constant<int, 2>{});
-    if (s + 3 < rows + 4) row_step(s + 3, std::integral_constant<int, 3>{});
-    if (s + 4 < rows + 4) row_step(s + 4, std::integral_constant<int, 4>{});
   }
 }
 
 template <int ACT>
 static void dw_launch_out(const DwArgs& a, int out_mode, dim3 grid, hipStream_t s) {
   switch (out_mode) {
-    case DW_MX_DYNAMIC: dw5x5_kernel<ACT, DW_MX_DYNAMIC><<<grid, dim3(256), 0, s>>>(a); break;
-    case DW_INT8: dw5x5_kernel<ACT, DW_INT8><<<grid, dim3(256), 0, s>>>(a); break;
-    case DW_BF16: dw5x5_kernel<ACT, DW_BF16><<<grid, dim3(256), 0, s>>>(a); break;
-    default: dw5x5_kernel<ACT, DW_MX_STATIC><<<grid, dim3(256), 0, s>>>(a); break;
+    case DW_MX_DYNAMIC: dw5x5_mfma_kernel<ACT, DW_MX_DYNAMIC><<<grid, dim3(256), 0, s>>>(a); break;
+    case DW_INT8: dw5x5_mfma_kernel<ACT, DW_INT8><<<grid, dim3(256), 0, s>>>(a); break;
+    case DW_BF16: dw5x5_mfma_kernel<ACT, DW_BF16><<<grid, dim3(256), 0, s>>>(a); break;
+    default: dw5x5_mfma_kernel<ACT, DW_MX_STATIC><<<grid, dim3(256), 0, s>>>(a); break;
   }
 }
 
