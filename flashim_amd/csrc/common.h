@@ -96,9 +96,12 @@ __device__ __forceinline__ float gelu_erf(float x) {
   p = fmaf(p, t, -5.615247726e+00f);
   p = fmaf(p, t, -1.334039974e+01f);
   p = fmaf(p, t, -9.062012672e+00f);  // the fit's constant -8.062 minus 1: the factor 1/2
+  // Below -5.53125 the exponent goes to -inf (the clamp argument is negative and scaled by 2^30 far past -149), so
+  // h = x * 0 = -0. h carries the sign of x, so x - h (x >= 0) and h (x < 0) are both max(x, -0) - |h|: no compare,
+  // no select, and the sign of zero follows torch (GELU(-0) = -0, the negative tail is -0).
+  p = fminf(p, fmaf(x, 0x1p30f, 5.53125f * 0x1p30f));
   const float h = x * __builtin_amdgcn_exp2f(p);
-  const float r = x < 0.0f ? h : x - h;
-  return x < -5.53125f ? -0.0f : r;
+  return __builtin_elementwise_maximum(x, -0.0f) - fabsf(h);
 }
 
 // Workgroup barrier for LDS hand-offs that leaves global loads in flight: waits only for this wave's LDS operations

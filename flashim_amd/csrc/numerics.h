@@ -204,9 +204,15 @@ __device__ __forceinline__ int8_t quantize_int8_fast(float x, float scale, float
 // two equals multiplication by its exact reciprocal (one rounding of the same real), so multiply.
 FIM_HD float mx_scale_clamp(float x, float inv_scale) {
   float q = x * inv_scale;
+#ifdef __HIP_DEVICE_COMPILE__
+  // IEEE 754-2019 minimum / maximum (v_minimum3_f32, v_maximum3_f32 on gfx950): NaN stays NaN as in torch's clamp,
+  // +-inf saturate, and no compare-select pair on VCC.
+  return __builtin_elementwise_maximum(__builtin_elementwise_minimum(q, 448.0f), -448.0f);
+#else
   q = q > 448.0f ? 448.0f : q;
   q = q < -448.0f ? -448.0f : q;
   return q;
+#endif
 }
 
 }  // namespace fim
