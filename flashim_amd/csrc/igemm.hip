@@ -694,6 +694,232 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
 }
 
 
+// Wide tiles: one workgroup of 8 wavefronts per CU over a (WM x 80) x (WN x 64) tile, WM x WN = 8 (160 x 256 or
+// 320 x 128), each wavefront 5 x 4 blocks of 16 x 16. Against two resident 128 x 128 workgroups per CU, a CU holds 25%
+// more outputs, every operand byte fetched from L2 feeds more MFMAs (config 2: 52 instead of 81 MB of L2 -> CU traffic
+// per launch), and the tile counts of large layers fill one round of CUs (config 2: 125 x 2 = 250 tiles on 256 CUs).
+// The accumulators take 80 VGPRs, so the operands bypass registers: each 8-row x 128-byte piece of a stage is one
+// wave-wide `buffer_load_dwordx4 ... lds` (lane l writes 16 bytes at LDS base + 16 l, so lane l fetches the global
+// segment that the XOR swizzle puts at that slot). Out-of-range offsets read as zero, which supplies the conv padding,
+// the rows past M and the channels past Cout without branches. Per K step: read this step's fragments from LDS, issue
+// the next step's loads into the other stage, run the MFMAs, then wait for the loads and barrier.
+// Requires 16-byte-aligned operands with Cin % 16 == 0, x and w below 2 GiB, per-channel MXFP8 activation exponents,
+// no pooling; the same MFMA per 16 x 16 block and K step, and the same epilogue, as the 128-row kernel.
+constexpr int WIDE_MB = 5, WIDE_NB = 4;
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ void vm_lds_barrier() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int KIND, int WM, int OUT>
+__global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs a) {
+  constexpr int WN = 8 / WM;
+  constexpr int MB = WIDE_MB, NB = WIDE_NB;
+  constexpr int BM = WM * MB * 16, BN = WN * NB * 16;
+  constexpr int STAGE = (BM + BN) * KC;
+  constexpr int CHUNKS = (BM + BN) / 8;  // 8 rows x 128 bytes: one wave-wide 16-byte-per-lane load
+  constexpr int CPW = (CHUNKS + 7) / 8;  // chunks per wavefront
+  static_assert(BM % 8 == 0 && BN % 8 == 0, "a chunk lies in one operand");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+  __shared__ __attribute__((aligned(16))) float ep_scale[BN], ep_bias[BN], ep_oinv[BN];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // provably uniform: the loads' LDS base and descriptor
+  const int wm = wave % WM, wn = wave / WM;
+
+  // XCD-aware order as in the 128-row kernel: each XCD takes a contiguous run of tiles, N tiles of an M tile adjacent
+  const int per_xcd = gridDim.x >> 3;
+  const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (t >= a.n_tiles * a.m_tiles) return;
+  const int n0 = (t % a.n_tiles) * BN;
+  const int m0 = a.m_base + (t / a.n_tiles) * BM;
+
+  if (tid < BN) {
+    const int n = n0 + tid;
+    const bool nok = n < a.Cout;
+    ep_scale[tid] = (KIND == KIND_INT8 && nok) ? *a.a_scale * a.w_scale[n] : 1.0f;
+    float bias = 0.0f;
+    if (a.bias != nullptr && nok)
+      bias = a.bias_dtype == FIM_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(a.bias)[n])
+                                      : static_cast<const float*>(a.bias)[n];
+    ep_bias[tid] = bias;
+    ep_oinv[tid] = (OUT == OUT_E4M3 && nok) ? exp2_int(-(int)a.out_expo[n >> 5]) : 1.0f;
+  }
+
+  const int wrow = a.kh * a.kw * a.Cin;  // < 2^31: the host bounds the weight bytes
+  const uint32_t x_bytes = (uint32_t)((int64_t)a.B * a.H * a.W * a.Cin);
+  const __amdgpu_buffer_rsrc_t x_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.x), (short)0, (int)x_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t w_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), (short)0, (int)((uint32_t)a.Cout * wrow), 0x00020000);
+  constexpr uint32_t OOB = 0x80000000u;  // past both buffers: reads as zero
+
+  // this lane's 16-byte segment in each of its wavefront's chunks: LDS row r = 8 c + lane / 8, slot lane % 8, holding
+  // global segment (lane % 8) ^ ((r / 2) % 8)
+  int ch_base[CPW], ch_h[CPW], ch_w[CPW], ch_cof[CPW];
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    const int c = wave + 8 * i;
+    const int r = 8 * c + (lane >> 3);
+    const int seg = (lane & 7) ^ ((r >> 1) & 7);
+    ch_cof[i] = seg * 16;
+    ch_h[i] = -(1 << 28);
+    ch_w[i] = 0;
+    ch_base[i] = 0;
+    if (c < CHUNKS && r < BM) {
+      const int m = m0 + r;
+      if (m < a.M) {
+        int img, oh, ow;
+        pixel_of_row<0>(a, m, img, oh, ow);
+        const int ih = oh * a.sh - a.ph, iw = ow * a.sw - a.pw;
+        ch_h[i] = ih;
+        ch_w[i] = iw;
+        ch_base[i] = ((img * a.H + ih) * a.W + iw) * a.Cin + seg * 16;
+      }
+    } else if (c < CHUNKS) {
+      const int n = n0 + r - BM;
+      ch_h[i] = n < a.Cout ? 0 : -(1 << 28);  // weight rows: only the row test applies
+      ch_base[i] = (n < a.Cout ? n : 0) * wrow + seg * 16;
+    }
+  }
+
+  const int g = lane >> 4;
+  int fr_x[MB], fr_w[NB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) {
+    const int r = wm * (MB * 16) + i * 16 + (lane & 15);
+    fr_x[i] = r * KC + ((g ^ ((r >> 1) & 7)) << 4);
+  }
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int r = BM + wn * (NB * 16) + i * 16 + (lane & 15);
+    fr_w[i] = r * KC + ((g ^ ((r >> 1) & 7)) << 4);
+  }
+  const int cblocks = a.Cin >> 5;
+  const int wexp_stride = wrow >> 5;
+  const int8_t* wexp_row[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int n = n0 + wn * (NB * 16) + i * 16 + (lane & 15);
+    wexp_row[i] = KIND == KIND_MX ? a.w_expo + (int64_t)(n < a.Cout ? n : 0) * wexp_stride : nullptr;
+  }
+
+  int ld_ky = 0, ld_kx = 0, ld_c0 = 0;
+  // issue the loads of the next (tap, channel chunk) step into LDS stage `buf`; its raw MX exponent bytes into (sx, sw)
+  auto issue = [&](int buf, int& sx, int (&sw)[NB], bool& ok) __attribute__((always_inline)) {
+    const int dy = ld_ky * a.dh, dx = ld_kx * a.dw;
+    const int xdelta = (dy * a.W + dx) * a.Cin + ld_c0;
+    const int wdelta = (ld_ky * a.kw + ld_kx) * a.Cin + ld_c0;
+    uint8_t* st = lds + buf * STAGE;
+#pragma unroll
+    for (int i = 0; i < CPW; ++i) {
+      const int c = wave + 8 * i;
+      if (c < CHUNKS) {  // uniform
+        const bool a_rows = 8 * c < BM;
+        const bool ok_c = ch_cof[i] < a.Cin - ld_c0;
+        const bool ok_r = a_rows ? ((unsigned)(ch_h[i] + dy) < (unsigned)a.H && (unsigned)(ch_w[i] + dx) < (unsigned)a.W)
+                                 : ch_h[i] == 0;
+        const uint32_t off = (ok_c && ok_r) ? (uint32_t)(ch_base[i] + (a_rows ? xdelta : wdelta)) : OOB;
+        if (a_rows)  // uniform; one descriptor per call keeps both in SGPRs
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rsrc, (lds_void_t*)(st + c * 1024), 16, off, 0, 0, 0);
+        else
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_void_t*)(st + c * 1024), 16, off, 0, 0, 0);
+      }
+    }
+    if (KIND == KIND_MX) {
+      const int blk = (ld_c0 >> 5) + g;
+      const int cblk = blk < cblocks ? blk : cblocks - 1;
+      sx = (int)a.x_expo[cblk];
+      ok = blk < cblocks;
+      const int wblk = (ld_ky * a.kw + ld_kx) * cblocks + cblk;
+#pragma unroll
+      for (int i = 0; i < NB; ++i) sw[i] = (int)wexp_row[i][wblk];
+    }
+    ld_c0 += KC;
+    if (ld_c0 >= a.Cin) {
+      ld_c0 = 0;
+      if (++ld_kx == a.kw) {
+        ld_kx = 0;
+        ++ld_ky;
+      }
+    }
+  };
+
+  v4i acc_i[NB][MB];
+  v4f acc_f[NB][MB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      acc_i[i][j] = v4i{0, 0, 0, 0};
+      acc_f[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    }
+
+  const int nk = a.kh * a.kw * a.kchunks;
+  int csx = 0, csw[NB];
+  bool cok = true;
+  issue(0, csx, csw, cok);
+  vm_lds_barrier();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const uint8_t* st = lds + (kt & 1) * STAGE;
+    // this step's fragments first: the next step's LDS-bound loads are issued after them, so no read waits on those
+    v4i xlo[MB], xhi[MB], wlo[NB], whi[NB];
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      xlo[j] = *reinterpret_cast<const v4i*>(st + fr_x[j]);
+      xhi[j] = *reinterpret_cast<const v4i*>(st + (fr_x[j] ^ 64));
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      wlo[i] = *reinterpret_cast<const v4i*>(st + fr_w[i]);
+      whi[i] = *reinterpret_cast<const v4i*>(st + (fr_w[i] ^ 64));
+    }
+    int sxs = 127, sw[NB];
+    if (KIND == KIND_MX) {
+      sxs = cok ? csx + 127 : 127;
+#pragma unroll
+      for (int i = 0; i < NB; ++i) sw[i] = cok ? csw[i] + 127 : 127;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (kt + 1 < nk) issue((kt + 1) & 1, csx, csw, cok);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (KIND == KIND_INT8) {
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+          acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wlo[i], xlo[j], acc_i[i][j], 0, 0, 0);
+          acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(whi[i], xhi[j], acc_i[i][j], 0, 0, 0);
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const v8i wf = __builtin_shufflevector(wlo[i], whi[i], 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+          const v8i xf = __builtin_shufflevector(xlo[j], xhi[j], 0, 1, 2, 3, 4, 5, 6, 7);
+          acc_f[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf, xf, acc_f[i][j], 0, 0, 0, sw[i], 0, sxs);
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the wait for the next stage stays behind this step's MFMAs
+    vm_lds_barrier();
+  }
+
+  conv_epilogue<KIND, OUT, 0, MB, NB>(a, acc_i, acc_f, m0 + wm * (MB * 16), n0, wn * (NB * 16), ep_scale, ep_bias,
+                                      ep_oinv);
+}
+
+template <int KIND, int WM>
+static void launch_wide(const ConvArgs& a, dim3 grid, hipStream_t stream) {
+  constexpr int QOUT = KIND == KIND_INT8 ? OUT_INT8 : OUT_E4M3;
+  if (a.out_mode == OUT_BF16)
+    conv_igemm_wide_kernel<KIND, WM, OUT_BF16><<<grid, dim3(512), 0, stream>>>(a);
+  else
+    conv_igemm_wide_kernel<KIND, WM, QOUT><<<grid, dim3(512), 0, stream>>>(a);
+}
+
 // 64 x 64 tiles (2 x 2 blocks per wavefront) on the plain path: the tail of a split launch, and launches too small to
 // reach every CU with 128-row tiles. With a.tps > 1 (Cin 16, 32, 64; 16-byte loads) the packed-tap variant.
 template <int KIND>
@@ -751,6 +977,22 @@ static void launch_xs(const ConvArgs& a, int lw, dim3 grid, hipStream_t stream) 
   launch_bn<KIND, BN, 0>(a, lw, grid, stream);
 }
 
+// Wide tiles (conv_igemm_wide_kernel) when they apply and their tiles fill at least 85% of their rounds of one
+// workgroup per CU; the wavefront grid is the one whose N tiles pad Cout the least (ties: 256-channel tiles).
+// Returns WM (2: 160 x 256 tiles, 4: 320 x 128) or 0.
+static int wide_wm(const ConvArgs& a, int lw) {
+#ifdef FIM_EXP_NO_WIDE
+  return 0;
+#endif
+  if (lw != 16 || a.x_swz != nullptr || a.pool_out != nullptr || a.a_scale_rows != nullptr || a.Cout <= 64) return 0;
+  if ((int64_t)a.B * a.H * a.W * a.Cin >= (1LL << 31) - 16 || (int64_t)a.Cout * a.kh * a.kw * a.Cin >= (1LL << 31))
+    return 0;
+  const int wm = cdiv((int64_t)a.Cout, 256) * 256 <= cdiv((int64_t)a.Cout, 128) * 128 ? 2 : 4;
+  const int64_t tiles = cdiv((int64_t)a.M, wm * 80) * cdiv((int64_t)a.Cout, (8 / wm) * 64);
+  const int64_t cus = device_cus();
+  return tiles * 100 >= cdiv(tiles, cus) * cus * 85 ? wm : 0;
+}
+
 template <int KIND>
 static int launch_conv(ConvArgs a, hipStream_t stream) {
   if (a.B < 0 || a.H < 0 || a.W < 0 || a.Cin <= 0 || a.Cout <= 0 || a.kh <= 0 || a.kw <= 0 || a.sh <= 0 ||
@@ -783,6 +1025,16 @@ static int launch_conv(ConvArgs a, hipStream_t stream) {
   if (tiles > (1LL << 30)) return FIM_ERR_UNSUPPORTED;
   a.m_tiles = (int)m_tiles;
   a.m_base = 0;
+  if (const int wm = wide_wm(a, lw)) {
+    a.n_tiles = (int)cdiv((int64_t)a.Cout, (8 / wm) * 64);
+    a.m_tiles = (int)cdiv((int64_t)a.M, wm * 80);
+    const dim3 grid((unsigned)(cdiv((int64_t)a.n_tiles * a.m_tiles, 8) * 8));
+    if (wm == 2)
+      launch_wide<KIND, 2>(a, grid, stream);
+    else
+      launch_wide<KIND, 4>(a, grid, stream);
+    return launch_status();
+  }
   // Workgroups stay resident 2 per CU, so tiles run in rounds of 2 x CUs. When the last round would be less than half
   // full (e.g. config 2: 632 tiles on 512 slots), it would still take a full tile time: the whole M tiles that fill
   // complete rounds run as one launch and the remaining rows as a second launch of 64 x 64 tiles (4x as many, each

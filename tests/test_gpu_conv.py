@@ -263,3 +263,75 @@ def test_split_launch_tail(kind):
     for r0 in (0, 128, 254, 256):  # slices in the first launch, across the boundary row 65536 = 256 x 256, the tail
         sl = run(x[:, r0:r0 + 4].contiguous())
         assert torch.equal(got[:, r0:r0 + 4].view(torch.int16), sl.view(torch.int16)), r0
+
+
+def _wide_cases():
+    """Shapes whose tiles fill one round of one wide (8-wavefront) workgroup per CU, so launch_conv picks the wide
+    kernel: 160 x 256 tiles for Cout 512 and 200 (the wavefront grid that pads Cout the least), 320 x 128 for
+    Cout 128. M is not a multiple of the tile height; Cin 32 leaves 96 of each 128-byte K step empty; Cout 200 runs
+    the general epilogue (Cout % 16 != 0) with a residual and quantized outputs, N tile 256 past Cout."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    return [
+        # (name, image (B, H, W), Cin, Cout, geometry, per-case kwargs)
+        ("1x1_c512", (1, 64, (cus // 2) * 160 // 64 - 1), 256, 512, (1, 1, 1, 1, 0, 0, 1, 1), {}),
+        ("3x3_c128", (1, 160, 2 * cus - 3), 32, 128, (3, 3, 1, 1, 1, 1, 1, 1), {}),
+        ("3x3_c200_res", (1, 128, cus * 160 // 128 - 1), 64, 200, (3, 3, 1, 1, 2, 2, 2, 2), {"residual": True}),
+    ]
+
+
+@pytest.mark.parametrize("case", range(3))
+def test_int8_conv2d_wide_tiles(case):
+    """INT8 through the wide kernel: bit-exact with the oracle (BF16 out, then INT8 out for the residual case)."""
+    name, shape, cin, cout, geo, kw = _wide_cases()[case]
+    x, weight, a_scale, w_scale, bias = _int8_inputs(cin, cout, geo[0], geo[1], True, shape=shape)
+    extra = {}
+    if kw.get("residual"):
+        extra["residual"] = (torch.randn(*shape[:3], cout) * 4).to(torch.bfloat16)
+    args = _dev(x, weight, a_scale, w_scale, bias)
+    got = ops.int8_conv2d.get("hip")(*args, *geo, relu=True, **{k: v.to(DEV) for k, v in extra.items()}).cpu()
+    assert torch.equal(got, ref.int8_conv2d(x, weight, a_scale, w_scale, bias, *geo, relu=True, **extra)), name
+    if extra:
+        out_scale = torch.tensor(0.07)
+        got_q = ops.int8_conv2d.get("hip")(*args, *geo, relu=True, residual=extra["residual"].to(DEV),
+                                           out_scale=out_scale.to(DEV)).cpu()
+        want_q = ref.int8_conv2d(x, weight, a_scale, w_scale, bias, *geo, relu=True, out_scale=out_scale, **extra)
+        assert torch.equal(got_q, want_q), name
+
+
+@pytest.mark.parametrize("case", range(3))
+def test_mxfp8_conv2d_wide_tiles(case):
+    """MXFP8 through the wide kernel, at sizes where one pre-activation BF16 flip (FP32 accumulation order) turns into
+    two BF16 steps after GELU's slope, so the activation is checked on its own: the plain conv meets the oracle bar;
+    GELU of it is torch's BF16 GELU of the same values within one BF16 step (2^-12 absolute in the cancelling tail);
+    + residual is that GELU output plus the residual rounded once, bit for bit; the 1x1 case's rows equal, bit for bit,
+    the same rows from small launches (4-row slices: another kernel, the same MFMA per 16 x 16 block and K step);
+    E4M3 output equals the BF16 output quantized separately."""
+    name, shape, cin, cout, geo, kw = _wide_cases()[case]
+    torch.manual_seed(case + 20)
+    x = (torch.randn(*shape, cin) * 3).to(torch.float8_e4m3fn)
+    ce = torch.randint(-6, 3, (cin // 32,), dtype=torch.int8)
+    w = (torch.randn(cout, geo[0] * geo[1] * cin) * 2).to(torch.float8_e4m3fn)
+    we = torch.randint(-9, -3, (cout, geo[0] * geo[1] * cin // 32), dtype=torch.int8)
+    bias = torch.randn(cout).to(torch.bfloat16)
+    run = lambda xs, **k: ops.mxfp8_conv2d.get("hip")(*_dev(xs, ce, w, we, bias), *geo, **k).cpu()  # noqa: E731
+    plain = run(x)
+    _assert_mx_close(plain, ref.mxfp8_conv2d(x, ce, w, we, bias, *geo))
+    got = run(x, gelu=True)
+    want = F.gelu(plain).float()
+    assert ((got.float() - want).abs() <= torch.clamp(want.abs() * 2**-7, min=2**-12)).all(), name
+    if kw.get("residual"):
+        r = torch.randn(*shape[:3], cout).to(torch.bfloat16)
+        got_r = run(x, gelu=True, residual=r.to(DEV))
+        assert torch.equal(got_r.view(torch.int16), (got.float() + r.float()).bfloat16().view(torch.int16)), name
+        got = got_r
+        extra = {"residual": r.to(DEV)}
+    else:
+        extra = {}
+    if geo[0] == 1:
+        for r0 in (0, 31, 60):
+            sl = run(x[:, r0:r0 + 4].contiguous(), gelu=True)
+            assert torch.equal(got[:, r0:r0 + 4].view(torch.int16), sl.view(torch.int16)), (name, r0)
+    if cout % 32 == 0:  # E4M3 outputs take whole 32-channel scale blocks
+        out_exponent = torch.randint(-3, 2, (cout // 32,), dtype=torch.int8)
+        got_q = run(x, gelu=True, out_exponent=out_exponent.to(DEV), **extra)
+        assert torch.equal(got_q.view(torch.uint8), ref.quantize_static(got, out_exponent).view(torch.uint8)), name
