@@ -144,8 +144,9 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
   const int g = lane >> 4;
   const float out_scale = OUT == OUT_INT8 ? *a.out_scale : 1.0f;
   const float out_inv = OUT == OUT_INT8 ? __fdiv_rn(1.0f, out_scale) : 1.0f;
-  const bool has_bias = a.bias != nullptr;
-  const bool relu_pre = a.relu_pre != 0;
+  // ReLU as IEEE maximum against 0 (on) or -inf (off: the identity, NaN kept): one operation, no select
+  float relu_lo = a.relu_pre != 0 ? 0.0f : -__builtin_inff();
+  asm("" : "+v"(relu_lo));  // opaque: otherwise the compiler folds the bound back into a per-value select
   const bool row_scales = KIND == KIND_INT8 && a.a_scale_rows != nullptr;
   const uint32_t nbytes = (uint32_t)a.M * (uint32_t)a.Cout * ESZ;
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(a.out, (short)0, (int)nbytes, 0x00020000);
@@ -171,8 +172,8 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
                          : __fmul_rn((float)acc_i[i][j][e], cs[e]);
         else
           t = acc_f[i][j][e];
-        t = has_bias ? __fadd_rn(t, cb[e]) : t;
-        v[e] = relu_pre ? fmaxf(t, 0.0f) : t;
+        t = __fadd_rn(t, cb[e]);  // the staged bias is -0 when there is none
+        v[e] = __builtin_elementwise_maximum(t, relu_lo);
       }
       round_bf16x2(v[0], v[1]);
       round_bf16x2(v[2], v[3]);
@@ -183,8 +184,10 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
 #endif
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
-        round_bf16x2(v[0], v[1]);
-        round_bf16x2(v[2], v[3]);
+        if (OUT != OUT_BF16) {  // a BF16 store packs with the same round-to-nearest-even
+          round_bf16x2(v[0], v[1]);
+          round_bf16x2(v[2], v[3]);
+        }
       }
     }
   }
@@ -430,7 +433,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
     const bool nok = n < a.Cout;
     ep_scale[tid] = (KIND == KIND_INT8 && nok) ? (a.a_scale_rows != nullptr ? a.w_scale[n] : *a.a_scale * a.w_scale[n])
                                                : 1.0f;
-    float bias = 0.0f;
+    float bias = -0.0f;  // x + (-0) == x for every x, -0 included: the fast epilogue adds it unconditionally
     if (a.bias != nullptr && nok)
       bias = a.bias_dtype == FIM_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(a.bias)[n])
                                       : static_cast<const float*>(a.bias)[n];
@@ -728,6 +731,7 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
   const int wm = wave % WM, wn = wave / WM;
 
   // XCD-aware order as in the 128-row kernel: each XCD takes a contiguous run of tiles, N tiles of an M tile adjacent
+  FIM_STAMP(0);
   const int per_xcd = gridDim.x >> 3;
   const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
   if (t >= a.n_tiles * a.m_tiles) return;
@@ -738,7 +742,7 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
     const int n = n0 + tid;
     const bool nok = n < a.Cout;
     ep_scale[tid] = (KIND == KIND_INT8 && nok) ? *a.a_scale * a.w_scale[n] : 1.0f;
-    float bias = 0.0f;
+    float bias = -0.0f;  // x + (-0) == x for every x, -0 included: the fast epilogue adds it unconditionally
     if (a.bias != nullptr && nok)
       bias = a.bias_dtype == FIM_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(a.bias)[n])
                                       : static_cast<const float*>(a.bias)[n];
@@ -860,6 +864,7 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
   bool cok = true;
   issue(0, csx, csw, cok);
   vm_lds_barrier();
+  FIM_STAMP(1);
 
   for (int kt = 0; kt < nk; ++kt) {
     const uint8_t* st = lds + (kt & 1) * STAGE;
@@ -907,8 +912,10 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
     vm_lds_barrier();
   }
 
+  FIM_STAMP(2);
   conv_epilogue<KIND, OUT, 0, MB, NB>(a, acc_i, acc_f, m0 + wm * (MB * 16), n0, wn * (NB * 16), ep_scale, ep_bias,
                                       ep_oinv);
+  FIM_STAMP(3);
 }
 
 template <int KIND, int WM>
