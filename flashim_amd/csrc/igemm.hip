@@ -131,10 +131,11 @@ __device__ __forceinline__ int pixel_of_row(const ConvArgs& a, int m, int& img, 
 // lane = pixel (lane & 15) of a 16-pixel block and 4 consecutive channels 4 (lane >> 4) + v of a 16-channel block, so
 // each store writes 4 channels of one pixel. row0: the wave's first GEMM row; n_tile0: the tile's first channel; nl0:
 // the wave's first channel within the tile (index into the per-channel operands ep_* staged in LDS).
-// Branch-free epilogue for the common case (no residual, no pooling, Cout % 16 == 0, output below 2 GiB): every value
-// of the wave is computed before the first store, so the per-value chains (GELU's above all) interleave, and outputs
-// past M or Cout are dropped by the buffer store's range check instead of per-lane branches. Same arithmetic, in the
-// same order per value, as the general epilogue below.
+// Branch-free epilogue for the common case (no residual, no pooling, Cout % 16 == 0, output below 2 GiB): per
+// 16-channel block column, all MB x 4 values of the lane are computed (their chains, GELU's above all, interleave) and
+// then stored, so the stores stream out while the next column is computed; outputs past M or Cout are dropped by the
+// buffer store's range check instead of per-lane branches. Same arithmetic, in the same order per value, as the
+// general epilogue below.
 template <int KIND, int OUT, int MB, int NB, bool GELU>
 __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
                                                    const v4f (&acc_f)[NB][MB], int row0, int n_tile0, int nl0,
@@ -148,12 +149,17 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
   float relu_lo = a.relu_pre != 0 ? 0.0f : -__builtin_inff();
   asm("" : "+v"(relu_lo));  // opaque: otherwise the compiler folds the bound back into a per-value select
   const bool row_scales = KIND == KIND_INT8 && a.a_scale_rows != nullptr;
-  const uint32_t nbytes = (uint32_t)a.M * (uint32_t)a.Cout * ESZ;
-  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(a.out, (short)0, (int)nbytes, 0x00020000);
+  // descriptor operands through readfirstlane: provably uniform, so the descriptor stays in SGPRs (a descriptor the
+  // compiler cannot prove uniform turns every store into a readfirstlane loop)
+  const int nbytes = __builtin_amdgcn_readfirstlane((int)((uint32_t)a.M * (uint32_t)a.Cout * ESZ));
+  const uint64_t out_addr = (uint64_t)a.out;
+  const uint64_t out_u = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(out_addr >> 32)) << 32) |
+                         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)out_addr);
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(out_u), (short)0, nbytes, 0x00020000);
   float arow[MB];
 #pragma unroll
   for (int j = 0; j < MB; ++j) arow[j] = row_scales ? a.a_scale_rows[min(row0 + j * 16 + (lane & 15), a.M - 1)] : 1.f;
-  float y[NB][MB][4];
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
     const int nl = nl0 + i * 16 + 4 * g;
@@ -161,9 +167,10 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
     const float4 cb4 = *reinterpret_cast<const float4*>(&ep_bias[nl]);
     const float cs[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
     const float cb[4] = {cb4.x, cb4.y, cb4.z, cb4.w};
+    float y[MB][4];
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
-      float* v = y[i][j];
+      float* v = y[j];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float t;
@@ -190,16 +197,12 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
         }
       }
     }
-  }
-#pragma unroll
-  for (int i = 0; i < NB; ++i) {
-    const int nl = nl0 + i * 16 + 4 * g;
     const int nbase = n_tile0 + nl;
     const bool nvalid = n_tile0 + nl0 + i * 16 < a.Cout;  // whole 16-channel block in or out (Cout % 16 == 0)
     const float4 ci4 = *reinterpret_cast<const float4*>(&ep_oinv[nl]);
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
-      const float* v = y[i][j];
+      const float* v = y[j];
       const int m = row0 + j * 16 + (lane & 15);
 #ifdef FIM_EPI_NOSTORE
       if (v[0] + v[1] + v[2] + v[3] == 12345.0f) static_cast<uint16_t*>(a.out)[m] = 1;
@@ -224,6 +227,9 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
         __builtin_amdgcn_raw_buffer_store_b32(pk, rsrc, (int)off, 0, 0);
       }
     }
+    // this block column's stores go out before the next one is computed, so the writes stream during the epilogue
+    // instead of draining after it
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -720,9 +726,15 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
   constexpr int BM = WM * MB * 16, BN = WN * NB * 16;
   constexpr int STAGE = (BM + BN) * KC;
   constexpr int CHUNKS = (BM + BN) / 8;  // 8 rows x 128 bytes: one wave-wide 16-byte-per-lane load
-  constexpr int CPW = (CHUNKS + 7) / 8;  // chunks per wavefront
+  constexpr int CPW = (CHUNKS + 7) / 8;  // chunks per wavefront (the first CHUNKS % 8 wavefronts take one more)
+  constexpr int CPW_MIN = CHUNKS / 8;
   static_assert(BM % 8 == 0 && BN % 8 == 0, "a chunk lies in one operand");
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+  // Three stages (loads two steps ahead) when they fit in the 160 KB of LDS next to the epilogue operands, else two.
+  // Each stage is its own array, so the compiler can tell a stage's reads from the loads in flight into the others.
+  constexpr int NST = 3 * STAGE + 3 * BN * 4 <= 163840 ? 3 : 2;
+  __shared__ __attribute__((aligned(16))) uint8_t st0[STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t st1[STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t st2[NST == 3 ? STAGE : 16];
   __shared__ __attribute__((aligned(16))) float ep_scale[BN], ep_bias[BN], ep_oinv[BN];
 
   const int tid = threadIdx.x;
@@ -735,6 +747,9 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
   const int per_xcd = gridDim.x >> 3;
   const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
   if (t >= a.n_tiles * a.m_tiles) return;
+#ifdef FIM_EXP_EMPTY
+  if (a.M > 0) return;
+#endif
   const int n0 = (t % a.n_tiles) * BN;
   const int m0 = a.m_base + (t / a.n_tiles) * BM;
 
@@ -751,11 +766,9 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
   }
 
   const int wrow = a.kh * a.kw * a.Cin;  // < 2^31: the host bounds the weight bytes
-  const uint32_t x_bytes = (uint32_t)((int64_t)a.B * a.H * a.W * a.Cin);
-  const __amdgpu_buffer_rsrc_t x_rsrc =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.x), (short)0, (int)x_bytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t w_rsrc =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), (short)0, (int)((uint32_t)a.Cout * wrow), 0x00020000);
+  // buffer sizes in bytes (< 2^31: checked by the host), through readfirstlane so the descriptors stay in SGPRs
+  const int x_nrec = __builtin_amdgcn_readfirstlane((int)((int64_t)a.B * a.H * a.W * a.Cin));
+  const int w_nrec = __builtin_amdgcn_readfirstlane(a.Cout * wrow);
   constexpr uint32_t OOB = 0x80000000u;  // past both buffers: reads as zero
 
   // this lane's 16-byte segment in each of its wavefront's chunks: LDS row r = 8 c + lane / 8, slot lane % 8, holding
@@ -810,11 +823,10 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
 
   int ld_ky = 0, ld_kx = 0, ld_c0 = 0;
   // issue the loads of the next (tap, channel chunk) step into LDS stage `buf`; its raw MX exponent bytes into (sx, sw)
-  auto issue = [&](int buf, int& sx, int (&sw)[NB], bool& ok) __attribute__((always_inline)) {
+  auto issue = [&](uint8_t* st, int& sx, int (&sw)[NB], bool& ok) __attribute__((always_inline)) {
     const int dy = ld_ky * a.dh, dx = ld_kx * a.dw;
     const int xdelta = (dy * a.W + dx) * a.Cin + ld_c0;
     const int wdelta = (ld_ky * a.kw + ld_kx) * a.Cin + ld_c0;
-    uint8_t* st = lds + buf * STAGE;
 #pragma unroll
     for (int i = 0; i < CPW; ++i) {
       const int c = wave + 8 * i;
@@ -824,10 +836,16 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
         const bool ok_r = a_rows ? ((unsigned)(ch_h[i] + dy) < (unsigned)a.H && (unsigned)(ch_w[i] + dx) < (unsigned)a.W)
                                  : ch_h[i] == 0;
         const uint32_t off = (ok_c && ok_r) ? (uint32_t)(ch_base[i] + (a_rows ? xdelta : wdelta)) : OOB;
-        if (a_rows)  // uniform; one descriptor per call keeps both in SGPRs
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rsrc, (lds_void_t*)(st + c * 1024), 16, off, 0, 0, 0);
+        // uniform branch; each call builds its descriptor from kernel arguments, so it is provably uniform (a
+        // descriptor the compiler cannot prove uniform turns every load into a readfirstlane loop)
+        if (a_rows)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.x), (short)0, x_nrec, 0x00020000),
+              (lds_void_t*)(st + c * 1024), 16, off, 0, 0, 0);
         else
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_void_t*)(st + c * 1024), 16, off, 0, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), (short)0, w_nrec, 0x00020000),
+              (lds_void_t*)(st + c * 1024), 16, off, 0, 0, 0);
       }
     }
     if (KIND == KIND_MX) {
@@ -860,35 +878,47 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
     }
 
   const int nk = a.kh * a.kw * a.kchunks;
-  int csx = 0, csw[NB];
-  bool cok = true;
-  issue(0, csx, csw, cok);
-  vm_lds_barrier();
-  FIM_STAMP(1);
+  int esx[NST], esw[NST][NB];
+  bool eok[NST];
+#pragma unroll
+  for (int s = 0; s < NST; ++s) {
+    esx[s] = 0;
+    eok[s] = true;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) esw[s][i] = 0;
+  }
 
-  for (int kt = 0; kt < nk; ++kt) {
-    const uint8_t* st = lds + (kt & 1) * STAGE;
-    // this step's fragments first: the next step's LDS-bound loads are issued after them, so no read waits on those
+  // one K step from stage `cur` (exponent set ec); the loads of step kt + NST - 1 go into stage `nxt` (set en)
+  auto step = [&](int kt, const uint8_t* cur, uint8_t* nxt, int ec, int en) __attribute__((always_inline)) {
+    // this step's fragments first: the next loads into LDS are issued after them, so no read waits on those
     v4i xlo[MB], xhi[MB], wlo[NB], whi[NB];
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
-      xlo[j] = *reinterpret_cast<const v4i*>(st + fr_x[j]);
-      xhi[j] = *reinterpret_cast<const v4i*>(st + (fr_x[j] ^ 64));
+      xlo[j] = *reinterpret_cast<const v4i*>(cur + fr_x[j]);
+      xhi[j] = *reinterpret_cast<const v4i*>(cur + (fr_x[j] ^ 64));
     }
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      wlo[i] = *reinterpret_cast<const v4i*>(st + fr_w[i]);
-      whi[i] = *reinterpret_cast<const v4i*>(st + (fr_w[i] ^ 64));
+      wlo[i] = *reinterpret_cast<const v4i*>(cur + fr_w[i]);
+      whi[i] = *reinterpret_cast<const v4i*>(cur + (fr_w[i] ^ 64));
     }
     int sxs = 127, sw[NB];
     if (KIND == KIND_MX) {
-      sxs = cok ? csx + 127 : 127;
+      sxs = eok[ec] ? esx[ec] + 127 : 127;
 #pragma unroll
-      for (int i = 0; i < NB; ++i) sw[i] = cok ? csw[i] + 127 : 127;
+      for (int i = 0; i < NB; ++i) sw[i] = eok[ec] ? esw[ec][i] + 127 : 127;
     }
+    const bool more = kt + NST - 1 < nk;
     __builtin_amdgcn_sched_barrier(0);
-    if (kt + 1 < nk) issue((kt + 1) & 1, csx, csw, cok);
+#ifndef FIM_EXP_NOLOAD
+    if (more) issue(nxt, esx[en], esw[en], eok[en]);
+#endif
     __builtin_amdgcn_sched_barrier(0);
+#ifdef FIM_EXP_NOMFMA
+    if (false) {
+#else
+    if (true) {
+#endif
     if constexpr (KIND == KIND_INT8) {
 #pragma unroll
       for (int i = 0; i < NB; ++i)
@@ -908,8 +938,41 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
         }
       }
     }
+    } else {
+#pragma unroll
+      for (int j = 0; j < MB; ++j) acc_f[0][j][0] += (float)(xlo[j][0] ^ xhi[j][1] ^ wlo[j % NB][2] ^ whi[j % NB][3]);
+    }
     __builtin_amdgcn_sched_barrier(0);  // the wait for the next stage stays behind this step's MFMAs
+    // step kt + 1's loads were issued one step earlier (or in the prologue); when this step issued loads, at least
+    // CPW_MIN of this wavefront's loads are younger than all of them, so vmcnt <= CPW_MIN means they have landed
+    if (NST == 3 && more)
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(CPW_MIN) : "memory");
+    else
+      vm_lds_barrier();
+  };
+
+  if constexpr (NST == 3) {
+    issue(st0, esx[0], esw[0], eok[0]);
+    if (nk > 1) {
+      issue(st1, esx[1], esw[1], eok[1]);
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(CPW_MIN) : "memory");
+    } else {
+      vm_lds_barrier();
+    }
+    FIM_STAMP(1);
+    for (int kt = 0; kt < nk; kt += 3) {
+      step(kt, st0, st2, 0, 2);
+      if (kt + 1 < nk) step(kt + 1, st1, st0, 1, 0);
+      if (kt + 2 < nk) step(kt + 2, st2, st1, 2, 1);
+    }
+  } else {
+    issue(st0, esx[0], esw[0], eok[0]);
     vm_lds_barrier();
+    FIM_STAMP(1);
+    for (int kt = 0; kt < nk; kt += 2) {
+      step(kt, st0, st1, 0, 1);
+      if (kt + 1 < nk) step(kt + 1, st1, st0, 1, 0);
+    }
   }
 
   FIM_STAMP(2);
