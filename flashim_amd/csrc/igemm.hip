@@ -132,10 +132,10 @@ __device__ __forceinline__ int pixel_of_row(const ConvArgs& a, int m, int& img, 
 // each store writes 4 channels of one pixel. row0: the wave's first GEMM row; n_tile0: the tile's first channel; nl0:
 // the wave's first channel within the tile (index into the per-channel operands ep_* staged in LDS).
 // Branch-free epilogue for the common case (no residual, no pooling, Cout % 16 == 0, output below 2 GiB): per
-// 16-channel block column, all MB x 4 values of the lane are computed (their chains, GELU's above all, interleave) and
-// then stored, so the stores stream out while the next column is computed; outputs past M or Cout are dropped by the
-// buffer store's range check instead of per-lane branches. Same arithmetic, in the same order per value, as the
-// general epilogue below.
+// 16-pixel row block, all NB x 4 values of the lane are computed (their chains, GELU's above all, interleave) and then
+// stored, so the stores stream out while the next block is computed, each burst covering whole lines; outputs past M
+// or Cout are dropped by the buffer store's range check instead of per-lane branches. Same arithmetic, in the same
+// order per value, as the general epilogue below.
 template <int KIND, int OUT, int MB, int NB, bool GELU>
 __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
                                                    const v4f (&acc_f)[NB][MB], int row0, int n_tile0, int nl0,
@@ -160,26 +160,32 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
   float arow[MB];
 #pragma unroll
   for (int j = 0; j < MB; ++j) arow[j] = row_scales ? a.a_scale_rows[min(row0 + j * 16 + (lane & 15), a.M - 1)] : 1.f;
+  float cs[NB][4], cb[NB][4], ci[NB][4];
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
     const int nl = nl0 + i * 16 + 4 * g;
     const float4 cs4 = *reinterpret_cast<const float4*>(&ep_scale[nl]);
     const float4 cb4 = *reinterpret_cast<const float4*>(&ep_bias[nl]);
-    const float cs[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
-    const float cb[4] = {cb4.x, cb4.y, cb4.z, cb4.w};
-    float y[MB][4];
+    const float4 ci4 = *reinterpret_cast<const float4*>(&ep_oinv[nl]);
+    cs[i][0] = cs4.x; cs[i][1] = cs4.y; cs[i][2] = cs4.z; cs[i][3] = cs4.w;
+    cb[i][0] = cb4.x; cb[i][1] = cb4.y; cb[i][2] = cb4.z; cb[i][3] = cb4.w;
+    ci[i][0] = ci4.x; ci[i][1] = ci4.y; ci[i][2] = ci4.z; ci[i][3] = ci4.w;
+  }
 #pragma unroll
-    for (int j = 0; j < MB; ++j) {
-      float* v = y[j];
+  for (int j = 0; j < MB; ++j) {
+    float y[NB][4];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      float* v = y[i];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float t;
         if (KIND == KIND_INT8)
-          t = row_scales ? __fmul_rn((float)acc_i[i][j][e], __fmul_rn(arow[j], cs[e]))
-                         : __fmul_rn((float)acc_i[i][j][e], cs[e]);
+          t = row_scales ? __fmul_rn((float)acc_i[i][j][e], __fmul_rn(arow[j], cs[i][e]))
+                         : __fmul_rn((float)acc_i[i][j][e], cs[i][e]);
         else
           t = acc_f[i][j][e];
-        t = __fadd_rn(t, cb[e]);  // the staged bias is -0 when there is none
+        t = __fadd_rn(t, cb[i][e]);  // the staged bias is -0 when there is none
         v[e] = __builtin_elementwise_maximum(t, relu_lo);
       }
       round_bf16x2(v[0], v[1]);
@@ -197,13 +203,12 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
         }
       }
     }
-    const int nbase = n_tile0 + nl;
-    const bool nvalid = n_tile0 + nl0 + i * 16 < a.Cout;  // whole 16-channel block in or out (Cout % 16 == 0)
-    const float4 ci4 = *reinterpret_cast<const float4*>(&ep_oinv[nl]);
+    const int m = row0 + j * 16 + (lane & 15);
 #pragma unroll
-    for (int j = 0; j < MB; ++j) {
-      const float* v = y[j];
-      const int m = row0 + j * 16 + (lane & 15);
+    for (int i = 0; i < NB; ++i) {
+      const float* v = y[i];
+      const int nbase = n_tile0 + nl0 + i * 16 + 4 * g;
+      const bool nvalid = n_tile0 + nl0 + i * 16 < a.Cout;  // whole 16-channel block in or out (Cout % 16 == 0)
 #ifdef FIM_EPI_NOSTORE
       if (v[0] + v[1] + v[2] + v[3] == 12345.0f) static_cast<uint16_t*>(a.out)[m] = 1;
       continue;
@@ -221,14 +226,14 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
 #pragma unroll
           for (int e = 0; e < 4; ++e) pk |= (uint32_t)(uint8_t)quantize_int8_fast(v[e], out_scale, out_inv) << (8 * e);
         } else {
-          pk = pack_e4m3x4(mx_scale_clamp(v[0], ci4.x), mx_scale_clamp(v[1], ci4.y), mx_scale_clamp(v[2], ci4.z),
-                           mx_scale_clamp(v[3], ci4.w));
+          pk = pack_e4m3x4(mx_scale_clamp(v[0], ci[i][0]), mx_scale_clamp(v[1], ci[i][1]),
+                           mx_scale_clamp(v[2], ci[i][2]), mx_scale_clamp(v[3], ci[i][3]));
         }
         __builtin_amdgcn_raw_buffer_store_b32(pk, rsrc, (int)off, 0, 0);
       }
     }
-    // this block column's stores go out before the next one is computed, so the writes stream during the epilogue
-    // instead of draining after it
+    // this row block's stores (all NB x 16 channels of 16 pixels: whole 128-byte lines of a BF16 output) go out before
+    // the next block is computed, so the writes stream during the epilogue and each line is written in one burst
     __builtin_amdgcn_sched_barrier(0);
   }
 }
