@@ -32,7 +32,7 @@ PEAK_HBM_GBS = 8000.0
 # HBM bytes per launch of the config-2 conv from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs (KiB per dispatch), each
 # scaled by what the counter reads for a plain 64 MiB device copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); the runs and the
 # arithmetic are in profiles/conv_mxfp8_1x1_gelu_cfg2.md. Re-measured by hand when the kernel changes.
-CFG2_TRAFFIC_BYTES = int((7477.9 * 2.0 + 20000.0 * 1.0) * 1024)  # both launches of the op (main + tail)
+CFG2_TRAFFIC_BYTES = int((6264.1 * 2.0 + 20000.0 * 1.0) * 1024)  # the op's one launch (wide-tile kernel)
 DEV = "cuda"
 
 
