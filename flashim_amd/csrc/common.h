@@ -85,8 +85,8 @@ __device__ __forceinline__ uint8_t e4m3(float a) {
 // 0.5% of the BF16 inputs, by one BF16 step, exactly as often as the exactly rounded GELU does (torch's own erf
 // rounding); in torch's cancelling negative tail (x < -3) both are within 2^-12 of each other.
 __device__ __forceinline__ float gelu_erf(float x) {
-  const float z = fminf(fabsf(x) * 0.70710678118654752440f, 4.1f);
-  const float t = fmaf(z, 0.48780487804878f, -1.0f);
+  // t = min(|x| / sqrt 2, 4.1) * 2 / 4.1 - 1 as one FMA and a clamp at t = 1
+  const float t = fminf(fmaf(fabsf(x), 0.70710678118654752440f * 0.48780487804878f, -1.0f), 1.0f);
   float p = -1.169777388e-04f;
   p = fmaf(p, t, -3.407272510e-03f);
   p = fmaf(p, t, 1.468000375e-02f);
