@@ -41,7 +41,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--only", default=None, help="run one workload only (cfg1|cfg2|cfg3|cfg3q|dw|stem|cfg4|cfg5int8|cfg5mxfp8|copy)"
+    p.add_argument("--only", default=None, help="run one workload only (cfg1|cfg2|cfg3|cfg3q|dw|stem|dwpw|cfg4|cfg5int8|cfg5mxfp8|copy)"
                                                   " and print its line (profiling runs)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-stack", action="store_true", help="skip configs 4 and 5")
@@ -197,6 +197,32 @@ def stem():
     return fn, {"bytes": pixels * 3 * 2 + pixels * 64}
 
 
+def dwpw_block():
+    """The depthwise-then-pointwise refiner blocks at the shape FlashIM times its fused kernels on (2 x 128 x 400 x 400,
+    flashim/backends/triton/conv.py:572-574): depthwise 5x5 + bias + ReLU -> dynamic MXFP8 / static INT8 -> 128 x 128
+    pointwise + bias -> BF16, as one kernel and as the two-launch composite. HBM bytes: BF16 in + BF16 out."""
+    from flashim_amd import ops, quant
+    from flashim_amd.backends.hip import conv as hip_conv
+
+    g = torch.Generator(device="cpu").manual_seed(10)
+    c = 128
+    x = (torch.randn(2, c, 400, 400, generator=g) * 2).to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
+    dw_w = (torch.randn(25, c, generator=g) * 0.3).to(torch.bfloat16)
+    dw_b, pw_b = torch.randn(c, generator=g), torch.randn(c, generator=g)
+    pw = quant.QuantizedWeight.from_float((torch.randn(c, c, generator=g) * 0.1).to(DEV))
+    mx = [t.to(DEV) for t in (x, dw_w, dw_b, pw.values, quant.swizzle_scales(pw.scale_exponent),
+                              quant.exponent_to_e8m0(pw.scale_exponent), pw_b)]
+    i8 = [t.to(DEV) for t in (x, dw_w, dw_b, torch.randint(-127, 128, (c, c), dtype=torch.int8, generator=g),
+                              torch.rand(c, generator=g) * 0.01 + 0.001, pw_b, torch.tensor(0.03))]
+    nbytes = 2 * 400 * 400 * c * 2 * 2
+    return {
+        "mxfp8_fused": lambda: ops.depthwise5x5_relu_pointwise_mxfp8(*mx),
+        "mxfp8_composite": lambda: hip_conv.pointwise_mxfp8_composite(*mx),
+        "int8_fused": lambda: ops.depthwise5x5_relu_pointwise_int8(*i8),
+        "int8_composite": lambda: hip_conv.pointwise_int8_composite(*i8),
+    }, {"bytes": nbytes}
+
+
 def copy_calibration():
     """A plain device copy of a known size (the PMC traffic calibration)."""
     src = torch.empty(64 << 20, device=DEV, dtype=torch.uint8).fill_(1)
@@ -288,6 +314,10 @@ def main() -> int:
     if only in (None, "stem"):
         fn, info = stem()
         hbm_line("stem_conv3x3_cin3_int8", fn, info)
+    if only in (None, "dwpw"):
+        fns, info = dwpw_block()
+        for name, fn in fns.items():
+            hbm_line(f"dwpw_2x128x400x400_{name}", fn, info)
     if not a.no_stack and only in (None, "cfg4", "cfg5int8", "cfg5mxfp8"):
         from flashim_amd import blocks
 

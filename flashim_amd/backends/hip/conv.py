@@ -246,10 +246,40 @@ def im2col_gather(x: Tensor, kh: int, kw: int, sh: int, sw: int, ph: int, pw: in
     return out
 
 
+def _fused_pointwise_shape(value: Tensor, pw_weight: Tensor) -> bool:
+    """The one-kernel block's shapes (``flashim/backends/triton/conv.py:561-599``): 128 channels in, 128 x 128
+    pointwise weight."""
+    return value.shape[1] == 128 and tuple(pw_weight.shape) == (128, 128)
+
+
 def depthwise5x5_relu_pointwise_mxfp8(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
                                       pw_scale_swizzled: Tensor, pw_scale_u8: Tensor, pw_bias: Tensor) -> Tensor:
-    """The MXFP8 refiner block (``flashim/ops/conv.py:93-113``): depthwise producer (dynamic MXFP8) then the
-    block-scaled pointwise GEMM with the weight's plain E8M0 bytes; ``[B, C, H, W]`` view of NHWC BF16."""
+    """The MXFP8 refiner block (``flashim/ops/conv.py:93-113``) -> ``[B, C, H, W]`` view of NHWC BF16. At 128 x 128
+    one kernel (``fim_depthwise5x5_relu_pointwise_mxfp8``: the quantized activations stay on chip), else the
+    composite."""
+    if not _fused_pointwise_shape(value, pw_weight):
+        return pointwise_mxfp8_composite(value, dw_weight, dw_bias, pw_weight, pw_scale_swizzled, pw_scale_u8,
+                                         pw_bias)
+    from flashim_amd.backends.hip import gemm
+
+    batch, channels, height, width = value.shape
+    x = _nhwc_bf16(value)
+    dw_w = dw_weight.to(device=value.device, dtype=torch.bfloat16).contiguous()
+    dw_b = dw_bias.to(device=value.device, dtype=torch.float32).contiguous()
+    e8m0 = pw_scale_u8.to(value.device).contiguous().view(torch.uint8)
+    bias, bias_code = gemm._bias(pw_bias, value.device)
+    out = torch.empty(batch, height, width, 128, device=value.device, dtype=torch.bfloat16)
+    _lib.call("fim_depthwise5x5_relu_pointwise_mxfp8", x.data_ptr(), batch, height, width, channels, dw_w.data_ptr(),
+              dw_b.data_ptr(), pw_weight.contiguous().view(torch.uint8).data_ptr(), 128, e8m0.data_ptr(),
+              _lib.ptr(bias), bias_code, out.data_ptr(), _lib.stream_of(value),
+              what=f"depthwise5x5_relu_pointwise_mxfp8 {tuple(value.shape)}")
+    return out.permute(0, 3, 1, 2)
+
+
+def pointwise_mxfp8_composite(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
+                              pw_scale_swizzled: Tensor, pw_scale_u8: Tensor, pw_bias: Tensor) -> Tensor:
+    """Two launches: depthwise producer (dynamic MXFP8) then the block-scaled pointwise GEMM with the weight's plain
+    E8M0 bytes."""
     from flashim_amd.backends.hip import gemm
 
     batch, channels, height, width = value.shape
@@ -267,7 +297,30 @@ def depthwise5x5_relu_pointwise_mxfp8(value: Tensor, dw_weight: Tensor, dw_bias:
 
 def depthwise5x5_relu_pointwise_int8(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
                                      pw_wscale: Tensor, pw_bias: Tensor, scale: Tensor) -> Tensor:
-    """The INT8 refiner block (``flashim/ops/conv.py:119-138``): static INT8 producer then ``int8_linear``."""
+    """The INT8 refiner block (``flashim/ops/conv.py:119-138``) -> ``[B, C, H, W]`` view of NHWC BF16. At 128 x 128
+    one kernel (``fim_depthwise5x5_relu_pointwise_int8``), else the composite."""
+    if not _fused_pointwise_shape(value, pw_weight):
+        return pointwise_int8_composite(value, dw_weight, dw_bias, pw_weight, pw_wscale, pw_bias, scale)
+    from flashim_amd.backends.hip import gemm
+
+    batch, channels, height, width = value.shape
+    x = _nhwc_bf16(value)
+    dw_w = dw_weight.to(device=value.device, dtype=torch.bfloat16).contiguous()
+    dw_b = dw_bias.to(device=value.device, dtype=torch.float32).contiguous()
+    wscale = pw_wscale.to(device=value.device, dtype=torch.float32).reshape(-1).contiguous()
+    a_scale = scale.to(device=value.device, dtype=torch.float32).reshape(1).contiguous()
+    bias, bias_code = gemm._bias(pw_bias, value.device)
+    out = torch.empty(batch, height, width, 128, device=value.device, dtype=torch.bfloat16)
+    _lib.call("fim_depthwise5x5_relu_pointwise_int8", x.data_ptr(), batch, height, width, channels, dw_w.data_ptr(),
+              dw_b.data_ptr(), pw_weight.contiguous().data_ptr(), 128, wscale.data_ptr(), a_scale.data_ptr(),
+              _lib.ptr(bias), bias_code, out.data_ptr(), _lib.stream_of(value),
+              what=f"depthwise5x5_relu_pointwise_int8 {tuple(value.shape)}")
+    return out.permute(0, 3, 1, 2)
+
+
+def pointwise_int8_composite(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
+                             pw_wscale: Tensor, pw_bias: Tensor, scale: Tensor) -> Tensor:
+    """Two launches: static INT8 producer then ``int8_linear``."""
     from flashim_amd.backends.hip import gemm
 
     batch, channels, height, width = value.shape

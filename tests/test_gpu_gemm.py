@@ -9,6 +9,7 @@ import torch
 import torch.nn.functional as F
 
 from flashim_amd import ops, quant
+from flashim_amd.backends.hip import conv as hip_conv
 from oracle import reference as ref
 
 pytestmark = pytest.mark.gpu
@@ -187,3 +188,30 @@ def test_depthwise_pointwise_mxfp8(batch, channels, hw):
     end_to_end = ref.depthwise5x5_relu_pointwise_mxfp8(*args).float()
     rel = (got.cpu().float() - end_to_end).norm() / end_to_end.norm()
     assert rel < 1e-2
+
+
+FUSED_BLOCK = [(1, (8, 32)), (2, (19, 45)), (1, (3, 5)), (2, (40, 70)), (1, (1, 1))]
+
+
+@pytest.mark.parametrize("batch,hw", FUSED_BLOCK)
+@pytest.mark.parametrize("bias", ["fp32", "bf16", "none"])
+def test_fused_depthwise_pointwise_matches_composite(batch, hw, bias):
+    """C = 128 with a 128 x 128 pointwise weight runs as one kernel (flashim/backends/triton/conv.py:310-508's
+    shapes): bit for bit the two-launch composite it replaces (same producer arithmetic, same MFMA per output block),
+    MXFP8 and INT8; tiles cut by the image edges, images smaller than the halo, every bias form."""
+    channels = 128
+    x, dw_w, dw_b, pw_b, g = _block_inputs(batch, channels, hw, seed=sum(hw) + batch)
+    pw_b = {"fp32": pw_b, "bf16": pw_b.to(torch.bfloat16), "none": None}[bias]
+    dev = lambda ts: [t.to(DEV) if t is not None else None for t in ts]  # noqa: E731
+    pw_w, pw_e = ref.quantized_weight_from_float(torch.randn(channels, channels, generator=g) * 0.1)
+    args = dev((x, dw_w, dw_b, pw_w, ref.swizzle_scales(pw_e), ref.exponent_to_e8m0(pw_e), pw_b))
+    fused = ops.depthwise5x5_relu_pointwise_mxfp8.get("hip")(*args)
+    composite = hip_conv.pointwise_mxfp8_composite(*args)
+    assert fused.shape == composite.shape == (batch, channels, *hw)
+    assert torch.equal(fused.view(torch.int16), composite.view(torch.int16))
+    pw_w8 = torch.randint(-127, 128, (channels, channels), dtype=torch.int8, generator=g)
+    pw_s = torch.rand(channels, generator=g) * 0.01 + 0.001
+    args = dev((x, dw_w, dw_b, pw_w8, pw_s, pw_b, torch.tensor(0.03)))
+    fused = ops.depthwise5x5_relu_pointwise_int8.get("hip")(*args)
+    composite = hip_conv.pointwise_int8_composite(*args)
+    assert torch.equal(fused.view(torch.int16), composite.view(torch.int16))
