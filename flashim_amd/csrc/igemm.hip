@@ -895,17 +895,32 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
 
   // one K step from stage `cur` (exponent set ec); the loads of step kt + NST - 1 go into stage `nxt` (set en)
   auto step = [&](int kt, const uint8_t* cur, uint8_t* nxt, int ec, int en) __attribute__((always_inline)) {
-    // this step's fragments first: the next loads into LDS are issued after them, so no read waits on those
+    // this step's fragments first: the next loads into LDS are issued after them, so no read waits on those. MXFP8
+    // operands are built as the 8-register tuples the MFMA reads, straight from their two LDS reads (built later,
+    // each tuple costs four 64-bit register moves per step)
     v4i xlo[MB], xhi[MB], wlo[NB], whi[NB];
+    v8i xf[MB], wf[NB];
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
-      xlo[j] = *reinterpret_cast<const v4i*>(cur + fr_x[j]);
-      xhi[j] = *reinterpret_cast<const v4i*>(cur + (fr_x[j] ^ 64));
+      const v4i lo = *reinterpret_cast<const v4i*>(cur + fr_x[j]);
+      const v4i hi = *reinterpret_cast<const v4i*>(cur + (fr_x[j] ^ 64));
+      if constexpr (KIND == KIND_MX) {
+        xf[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      } else {
+        xlo[j] = lo;
+        xhi[j] = hi;
+      }
     }
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      wlo[i] = *reinterpret_cast<const v4i*>(cur + fr_w[i]);
-      whi[i] = *reinterpret_cast<const v4i*>(cur + (fr_w[i] ^ 64));
+      const v4i lo = *reinterpret_cast<const v4i*>(cur + fr_w[i]);
+      const v4i hi = *reinterpret_cast<const v4i*>(cur + (fr_w[i] ^ 64));
+      if constexpr (KIND == KIND_MX) {
+        wf[i] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      } else {
+        wlo[i] = lo;
+        whi[i] = hi;
+      }
     }
     int sxs = 127, sw[NB];
     if (KIND == KIND_MX) {
@@ -934,18 +949,14 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
         }
     } else {
 #pragma unroll
-      for (int i = 0; i < NB; ++i) {
-        const v8i wf = __builtin_shufflevector(wlo[i], whi[i], 0, 1, 2, 3, 4, 5, 6, 7);
+      for (int i = 0; i < NB; ++i)
 #pragma unroll
-        for (int j = 0; j < MB; ++j) {
-          const v8i xf = __builtin_shufflevector(xlo[j], xhi[j], 0, 1, 2, 3, 4, 5, 6, 7);
-          acc_f[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf, xf, acc_f[i][j], 0, 0, 0, sw[i], 0, sxs);
-        }
-      }
+        for (int j = 0; j < MB; ++j)
+          acc_f[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[i], xf[j], acc_f[i][j], 0, 0, 0, sw[i], 0, sxs);
     }
     } else {
 #pragma unroll
-      for (int j = 0; j < MB; ++j) acc_f[0][j][0] += (float)(xlo[j][0] ^ xhi[j][1] ^ wlo[j % NB][2] ^ whi[j % NB][3]);
+      for (int j = 0; j < MB; ++j) acc_f[0][j][0] += (float)(xf[j][0] ^ xlo[j][0] ^ wf[j % NB][2] ^ wlo[j % NB][3]);
     }
     __builtin_amdgcn_sched_barrier(0);  // the wait for the next stage stays behind this step's MFMAs
     // step kt + 1's loads were issued one step earlier (or in the prologue); when this step issued loads, at least
