@@ -136,7 +136,10 @@ __device__ __forceinline__ int pixel_of_row(const ConvArgs& a, int m, int& img, 
 // stored, so the stores stream out while the next block is computed, each burst covering whole lines; outputs past M
 // or Cout are dropped by the buffer store's range check instead of per-lane branches. Same arithmetic, in the same
 // order per value, as the general epilogue below.
-template <int KIND, int OUT, int MB, int NB, bool GELU>
+// RES: a BF16 residual laid out as the output ([M, Cout] dense, so its element offset is the output's), added after
+// the activation with the conv semantics relu(y + r) (ops/conv.py:198-203): loaded per row block with the same
+// out-of-range handling as the stores.
+template <int KIND, int OUT, int MB, int NB, bool GELU, bool RES = false>
 __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
                                                    const v4f (&acc_f)[NB][MB], int row0, int n_tile0, int nl0,
                                                    const float* ep_scale, const float* ep_bias, const float* ep_oinv) {
@@ -157,6 +160,18 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
                          (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)out_addr);
   const __amdgpu_buffer_rsrc_t rsrc =
       __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(out_u), (short)0, nbytes, 0x00020000);
+  __amdgpu_buffer_rsrc_t res_rsrc = rsrc;
+  float relu_post_lo = -__builtin_inff();
+  if constexpr (RES) {
+    const uint64_t res_addr = (uint64_t)a.residual;
+    const uint64_t res_u = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(res_addr >> 32)) << 32) |
+                           (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)res_addr);
+    res_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<void*>(res_u), (short)0,
+        __builtin_amdgcn_readfirstlane((int)((uint32_t)a.M * (uint32_t)a.Cout * 2)), 0x00020000);
+    relu_post_lo = a.relu_post != 0 ? 0.0f : -__builtin_inff();
+    asm("" : "+v"(relu_post_lo));
+  }
   float arow[MB];
 #pragma unroll
   for (int j = 0; j < MB; ++j) arow[j] = row_scales ? a.a_scale_rows[min(row0 + j * 16 + (lane & 15), a.M - 1)] : 1.f;
@@ -173,6 +188,18 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
   }
 #pragma unroll
   for (int j = 0; j < MB; ++j) {
+    const int m = row0 + j * 16 + (lane & 15);
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    u32x2 rv[NB];
+    if constexpr (RES) {  // this row block's residual, in flight while its values are computed
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const bool nvalid = n_tile0 + nl0 + i * 16 < a.Cout;
+        const uint32_t roff =
+            nvalid ? ((uint32_t)m * (uint32_t)a.Cout + (uint32_t)(n_tile0 + nl0 + i * 16 + 4 * g)) * 2 : 0x80000000u;
+        rv[i] = __builtin_amdgcn_raw_buffer_load_b64(res_rsrc, (int)roff, 0, 0);
+      }
+    }
     float y[NB][4];
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
@@ -197,13 +224,22 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
 #endif
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
-        if (OUT != OUT_BF16) {  // a BF16 store packs with the same round-to-nearest-even
+        if (RES || OUT != OUT_BF16) {  // a BF16 store packs with the same round-to-nearest-even
+          round_bf16x2(v[0], v[1]);
+          round_bf16x2(v[2], v[3]);
+        }
+      }
+      if constexpr (RES) {  // relu(y + r) in FP32, then BF16 (a BF16 store's pack rounds)
+        v[0] = __builtin_elementwise_maximum(__fadd_rn(v[0], u2f(rv[i][0] << 16)), relu_post_lo);
+        v[1] = __builtin_elementwise_maximum(__fadd_rn(v[1], u2f(rv[i][0] & 0xffff0000u)), relu_post_lo);
+        v[2] = __builtin_elementwise_maximum(__fadd_rn(v[2], u2f(rv[i][1] << 16)), relu_post_lo);
+        v[3] = __builtin_elementwise_maximum(__fadd_rn(v[3], u2f(rv[i][1] & 0xffff0000u)), relu_post_lo);
+        if (OUT != OUT_BF16) {
           round_bf16x2(v[0], v[1]);
           round_bf16x2(v[2], v[3]);
         }
       }
     }
-    const int m = row0 + j * 16 + (lane & 15);
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const float* v = y[i];
@@ -217,7 +253,6 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
       const uint32_t off = nvalid ? ((uint32_t)m * (uint32_t)a.Cout + (uint32_t)nbase) * ESZ : 0x80000000u;
       if (OUT == OUT_BF16) {
         const uint32_t lo = pack_bf16x2(v[0], v[1]), hi = pack_bf16x2(v[2], v[3]);
-        typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
         __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rsrc, (int)off, 0, 0);
       } else {
         uint32_t pk;
@@ -242,12 +277,25 @@ template <int KIND, int OUT, int POOL, int MB, int NB>
 __device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc_i)[NB][MB], const v4f (&acc_f)[NB][MB],
                                               int row0, int n_tile0, int nl0, const float* ep_scale,
                                               const float* ep_bias, const float* ep_oinv) {
-  if (!POOL && a.residual == nullptr && (a.Cout & 15) == 0 &&
+  // a residual in the output's own dense BF16 layout (the refiner blocks' contract convs) stays on the fast path
+  const bool res_dense = a.residual != nullptr && a.res_dtype == FIM_BF16 && a.res_channels == a.Cout && a.rs_c == 1 &&
+                         a.rs_w == a.Cout && a.rs_h == (int64_t)a.Wo * a.Cout &&
+                         a.rs_b == (int64_t)a.Ho * a.Wo * a.Cout && ((uintptr_t)a.residual & 7) == 0 &&
+                         (int64_t)a.M * a.Cout * 2 < (int64_t)0x7fffffff;
+  if (!POOL && (a.residual == nullptr || res_dense) && (a.Cout & 15) == 0 &&
       (int64_t)a.M * a.Cout * (OUT == OUT_BF16 ? 2 : 1) < (int64_t)0x7fffffff) {
-    if (a.gelu)
+    if (a.residual != nullptr) {
+      if (a.gelu)
+        conv_epilogue_fast<KIND, OUT, MB, NB, true, true>(a, acc_i, acc_f, row0, n_tile0, nl0, ep_scale, ep_bias,
+                                                          ep_oinv);
+      else
+        conv_epilogue_fast<KIND, OUT, MB, NB, false, true>(a, acc_i, acc_f, row0, n_tile0, nl0, ep_scale, ep_bias,
+                                                           ep_oinv);
+    } else if (a.gelu) {
       conv_epilogue_fast<KIND, OUT, MB, NB, true>(a, acc_i, acc_f, row0, n_tile0, nl0, ep_scale, ep_bias, ep_oinv);
-    else
+    } else {
       conv_epilogue_fast<KIND, OUT, MB, NB, false>(a, acc_i, acc_f, row0, n_tile0, nl0, ep_scale, ep_bias, ep_oinv);
+    }
     return;
   }
   const int lane = threadIdx.x & 63;

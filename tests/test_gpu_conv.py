@@ -335,3 +335,54 @@ def test_mxfp8_conv2d_wide_tiles(case):
         out_exponent = torch.randint(-3, 2, (cout // 32,), dtype=torch.int8)
         got_q = run(x, gelu=True, out_exponent=out_exponent.to(DEV), **extra)
         assert torch.equal(got_q.view(torch.uint8), ref.quantize_static(got, out_exponent).view(torch.uint8)), name
+
+
+@pytest.mark.parametrize("kind", ["int8", "mxfp8"])
+@pytest.mark.parametrize("gelu", [False, True])
+@pytest.mark.parametrize("wide", [False, True])
+def test_dense_residual_fast_epilogue(kind, gelu, wide):
+    """A residual laid out as the output ([B, Ho, Wo, Cout] BF16, Cout % 16 == 0: the refiner blocks' contract convs)
+    runs on the fast epilogue: INT8 without GELU bit-exact with the oracle (BF16 and INT8 out); otherwise bit-exact
+    with relu(y + r) rounded once, y the same conv's output without the residual, y at the oracle bar (GELU: within one
+    BF16 step). 128-row tiles, and a one-round launch of the wide kernel."""
+    torch.manual_seed(31 + 2 * gelu + wide)
+    if wide:
+        cus = torch.cuda.get_device_properties(0).multi_processor_count
+        shape, cin, cout, geo = (1, 64, (cus // 2) * 160 // 64 - 1), 128, 512, (1, 1, 1, 1, 0, 0, 1, 1)
+    else:
+        shape, cin, cout, geo = (2, 17, 19), 64, 96, (3, 3, 1, 1, 1, 1, 1, 1)
+    r = (torch.randn(*shape, cout) * 2).to(torch.bfloat16)
+    if kind == "int8":
+        x, w, a_scale, w_scale, bias = _int8_inputs(cin, cout, geo[0], geo[1], True, shape=shape)
+        args = _dev(x, w, a_scale, w_scale, bias)
+        run = lambda **k: ops.int8_conv2d.get("hip")(*args, *geo, gelu=gelu, **k).cpu()  # noqa: E731
+        got = run(relu=True, residual=r.to(DEV))
+        out_scale = torch.tensor(0.05)
+        got_q = run(relu=True, residual=r.to(DEV), out_scale=out_scale.to(DEV))
+        if not gelu:
+            assert torch.equal(got, ref.int8_conv2d(x, w, a_scale, w_scale, bias, *geo, relu=True, residual=r))
+            assert torch.equal(got_q, ref.int8_conv2d(x, w, a_scale, w_scale, bias, *geo, relu=True, residual=r,
+                                                      out_scale=out_scale))
+        else:  # this GELU is within one BF16 step of torch's: pin y there, the residual add by the exact identity
+            y = run()
+            want_y = ref.int8_conv2d(x, w, a_scale, w_scale, bias, *geo, gelu=True)
+            assert ((y.float() - want_y.float()).abs() <= want_y.float().abs() * 2**-7 + 2**-12).all()
+            assert torch.equal(got.view(torch.int16), torch.relu(y.float() + r.float()).bfloat16().view(torch.int16))
+            assert torch.equal(got_q, ref.quantize_int8_static(got, out_scale))
+    else:
+        x = (torch.randn(*shape, cin) * 3).to(torch.float8_e4m3fn)
+        ce = torch.randint(-6, 3, (cin // 32,), dtype=torch.int8)
+        w = (torch.randn(cout, geo[0] * geo[1] * cin) * 2).to(torch.float8_e4m3fn)
+        we = torch.randint(-9, -3, (cout, geo[0] * geo[1] * cin // 32), dtype=torch.int8)
+        bias = torch.randn(cout).to(torch.bfloat16)
+        run = lambda **k: ops.mxfp8_conv2d.get("hip")(*_dev(x, ce, w, we, bias), *geo, gelu=gelu, **k).cpu()  # noqa: E731
+        plain = run()
+        got = run(relu=True, residual=r.to(DEV))
+        want = torch.relu(plain.float() + r.float()).bfloat16()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+        if not gelu:  # y itself at the oracle bar (a cancelling residual would turn one FP32-order flip of y into
+            # more than the bar's relative term of the small sum: the identity above pins the residual add)
+            _assert_mx_close(plain, ref.mxfp8_conv2d(x, ce, w, we, bias, *geo))
+        out_exponent = torch.randint(-3, 2, (cout // 32,), dtype=torch.int8)
+        got_q = run(relu=True, residual=r.to(DEV), out_exponent=out_exponent.to(DEV))
+        assert torch.equal(got_q.view(torch.uint8), ref.quantize_static(got, out_exponent).view(torch.uint8))
