@@ -70,6 +70,33 @@ __device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float
 #endif
 }
 
+// E4M3 codes of BF16(a..d) * 2^-e, clamped to +-448: the BF16 rounding then static MXFP8 quantize of the references
+// (a BF16 activation quantized with quant/tensor.py:97-121). scale = 2^e, bound = 448 * 2^e. The clamp commutes with
+// the BF16 rounding (bound is a BF16 value and rounding is monotonic), so the values are clamped in FP32 (IEEE
+// minimum / maximum: NaN stays NaN), rounded to BF16 by the pack, and v_cvt_scalef32_pk_fp8_bf16 divides by the scale
+// and converts: 2 operations per value fewer than unpacking, multiplying and converting from FP32, and byte for byte
+// the same codes (measured on the GPU over every BF16 input, NaN and infinities included, at exponents -10..10).
+__device__ __forceinline__ uint32_t e4m3x4_of_bf16(float a, float b, float c, float d, float scale, float bound) {
+  a = __builtin_elementwise_maximum(__builtin_elementwise_minimum(a, bound), -bound);
+  b = __builtin_elementwise_maximum(__builtin_elementwise_minimum(b, bound), -bound);
+  c = __builtin_elementwise_maximum(__builtin_elementwise_minimum(c, bound), -bound);
+  d = __builtin_elementwise_maximum(__builtin_elementwise_minimum(d, bound), -bound);
+#ifdef FIM_SOFTWARE_E4M3
+  round_bf16x2(a, b);
+  round_bf16x2(c, d);
+  const float inv = 1.0f / scale;  // exact: a power of two
+  return pack_e4m3x4(a * inv, b * inv, c * inv, d * inv);
+#else
+  typedef short v2s_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 v2bf_t __attribute__((ext_vector_type(2)));
+  const v2s_t lo = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(v2s_t{0, 0}, __builtin_bit_cast(v2bf_t, pack_bf16x2(a, b)),
+                                                             scale, false);
+  const v2s_t both = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(lo, __builtin_bit_cast(v2bf_t, pack_bf16x2(c, d)),
+                                                               scale, true);
+  return __builtin_bit_cast(uint32_t, both);
+#endif
+}
+
 __device__ __forceinline__ uint8_t e4m3(float a) {
 #ifdef FIM_SOFTWARE_E4M3
   return f32_to_e4m3_sw(a);
@@ -104,6 +131,30 @@ __device__ __forceinline__ float gelu_erf(float x) {
   p = fminf(p, fmaf(x, 0x1p30f, 5.53125f * 0x1p30f));
   const float h = x * __builtin_amdgcn_exp2f(p);
   return __builtin_elementwise_maximum(x, -0.0f) - fabsf(h);
+}
+
+// gelu_erf over N independent values, written step by step (each Horner step over all N values before the next), so
+// the N dependent chains interleave: the compiler otherwise schedules a value's whole chain before the next value's,
+// two at a time, and the VALU waits on the chain latency. Same arithmetic per value as gelu_erf.
+template <int N>
+__device__ __forceinline__ void gelu_erf_n(float (&x)[N]) {
+  constexpr float kS = 0.3224875f;
+  constexpr float kC[7] = {13.051149f, -10.621295f, 7.961414f, -5.8366094f, -53.993702f, -41.367184f, -9.062012672f};
+  float u[N], p[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) u[i] = fminf(fmaf(fabsf(x[i]), 0.70710678118654752440f * 0.48780487804878f * kS, -kS), kS);
+#pragma unroll
+  for (int i = 0; i < N; ++i) p[i] = -9.393265f - u[i];
+#pragma unroll
+  for (int k = 0; k < 7; ++k)
+#pragma unroll
+    for (int i = 0; i < N; ++i) p[i] = fmaf(p[i], u[i], kC[k]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) p[i] = fminf(p[i], fmaf(x[i], 0x1p30f, 5.53125f * 0x1p30f));
+#pragma unroll
+  for (int i = 0; i < N; ++i) p[i] = x[i] * __builtin_amdgcn_exp2f(p[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) x[i] = __builtin_elementwise_maximum(x[i], -0.0f) - fabsf(p[i]);
 }
 
 // Workgroup barrier for LDS hand-offs that leaves global loads in flight: waits only for this wave's LDS operations

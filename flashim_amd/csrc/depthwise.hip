@@ -161,8 +161,10 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
         round_bf16x2(v[2], v[3]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = gelu_erf(v[i]);
-        round_bf16x2(v[0], v[1]);
-        round_bf16x2(v[2], v[3]);
+        if (OUT != DW_MX_STATIC) {  // static MXFP8 rounds to BF16 in its conversion (e4m3x4_of_bf16)
+          round_bf16x2(v[0], v[1]);
+          round_bf16x2(v[2], v[3]);
+        }
       }
   }
 
@@ -171,7 +173,11 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
     oscale = *a.scale;
     oinv8 = __fdiv_rn(1.0f, oscale);
   }
-  if (OUT == DW_MX_STATIC) oinv = exp2_int(-(int)a.expo[cbase >> 5]);
+  float osc = 1.f;
+  if (OUT == DW_MX_STATIC) {
+    oinv = exp2_int(-(int)a.expo[cbase >> 5]);
+    osc = exp2_int((int)a.expo[cbase >> 5]);
+  }
   const int64_t groups = a.C >> 5;
   const int64_t tiles_k = (groups + 3) >> 2;
   const int rows = min(DW_TH, a.H - y0), cols = min(DW_TW, a.W - x0);
@@ -243,12 +249,17 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
           *reinterpret_cast<uint2*>(static_cast<uint8_t*>(a.out) + row * a.C + c) = make_uint2(q0, q1);
         }
       } else if (OUT == DW_MX_STATIC) {
-        if (ok)
-          *reinterpret_cast<uint2*>(static_cast<uint8_t*>(a.out) + row * a.C + c) =
-              make_uint2(pack_e4m3x4(mx_scale_clamp(v[0], oinv), mx_scale_clamp(v[1], oinv),
-                                     mx_scale_clamp(v[2], oinv), mx_scale_clamp(v[3], oinv)),
-                         pack_e4m3x4(mx_scale_clamp(v[4], oinv), mx_scale_clamp(v[5], oinv),
-                                     mx_scale_clamp(v[6], oinv), mx_scale_clamp(v[7], oinv)));
+        uint2 codes;
+        if (ACT == ACT_GELU) {  // BF16 rounding and static E4M3 in one step (the values arrive unrounded)
+          codes = make_uint2(e4m3x4_of_bf16(v[0], v[1], v[2], v[3], osc, 448.0f * osc),
+                             e4m3x4_of_bf16(v[4], v[5], v[6], v[7], osc, 448.0f * osc));
+        } else {
+          codes = make_uint2(pack_e4m3x4(mx_scale_clamp(v[0], oinv), mx_scale_clamp(v[1], oinv),
+                                         mx_scale_clamp(v[2], oinv), mx_scale_clamp(v[3], oinv)),
+                             pack_e4m3x4(mx_scale_clamp(v[4], oinv), mx_scale_clamp(v[5], oinv),
+                                         mx_scale_clamp(v[6], oinv), mx_scale_clamp(v[7], oinv)));
+        }
+        if (ok) *reinterpret_cast<uint2*>(static_cast<uint8_t*>(a.out) + row * a.C + c) = codes;
       } else {
         if (ok)
           *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + row * a.C + c) =

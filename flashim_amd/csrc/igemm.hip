@@ -142,7 +142,7 @@ __device__ __forceinline__ int pixel_of_row(const ConvArgs& a, int m, int& img, 
 template <int KIND, int OUT, int MB, int NB, bool GELU, bool RES = false>
 __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
                                                    const v4f (&acc_f)[NB][MB], int row0, int n_tile0, int nl0,
-                                                   const float* ep_scale, const float* ep_bias, const float* ep_oinv) {
+                                                   const float* ep_scale, const float* ep_bias, const float* ep_osc) {
   constexpr int ESZ = OUT == OUT_BF16 ? 2 : 1;
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4;
@@ -175,16 +175,15 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
   float arow[MB];
 #pragma unroll
   for (int j = 0; j < MB; ++j) arow[j] = row_scales ? a.a_scale_rows[min(row0 + j * 16 + (lane & 15), a.M - 1)] : 1.f;
-  float cs[NB][4], cb[NB][4], ci[NB][4];
+  float cs[NB][4], cb[NB][4], osc[NB];
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
     const int nl = nl0 + i * 16 + 4 * g;
     const float4 cs4 = *reinterpret_cast<const float4*>(&ep_scale[nl]);
     const float4 cb4 = *reinterpret_cast<const float4*>(&ep_bias[nl]);
-    const float4 ci4 = *reinterpret_cast<const float4*>(&ep_oinv[nl]);
     cs[i][0] = cs4.x; cs[i][1] = cs4.y; cs[i][2] = cs4.z; cs[i][3] = cs4.w;
     cb[i][0] = cb4.x; cb[i][1] = cb4.y; cb[i][2] = cb4.z; cb[i][3] = cb4.w;
-    ci[i][0] = ci4.x; ci[i][1] = ci4.y; ci[i][2] = ci4.z; ci[i][3] = ci4.w;
+    osc[i] = ep_osc[nl];  // the lane's 4 channels (aligned by 4) share one 32-channel scale block
   }
 #pragma unroll
   for (int j = 0; j < MB; ++j) {
@@ -224,7 +223,7 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
 #endif
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
-        if (RES || OUT != OUT_BF16) {  // a BF16 store packs with the same round-to-nearest-even
+        if (RES || OUT == OUT_INT8) {  // a BF16 store's pack and the E4M3 conversion round the same way
           round_bf16x2(v[0], v[1]);
           round_bf16x2(v[2], v[3]);
         }
@@ -234,7 +233,7 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
         v[1] = __builtin_elementwise_maximum(__fadd_rn(v[1], u2f(rv[i][0] & 0xffff0000u)), relu_post_lo);
         v[2] = __builtin_elementwise_maximum(__fadd_rn(v[2], u2f(rv[i][1] << 16)), relu_post_lo);
         v[3] = __builtin_elementwise_maximum(__fadd_rn(v[3], u2f(rv[i][1] & 0xffff0000u)), relu_post_lo);
-        if (OUT != OUT_BF16) {
+        if (OUT == OUT_INT8) {
           round_bf16x2(v[0], v[1]);
           round_bf16x2(v[2], v[3]);
         }
@@ -261,8 +260,7 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
 #pragma unroll
           for (int e = 0; e < 4; ++e) pk |= (uint32_t)(uint8_t)quantize_int8_fast(v[e], out_scale, out_inv) << (8 * e);
         } else {
-          pk = pack_e4m3x4(mx_scale_clamp(v[0], ci[i][0]), mx_scale_clamp(v[1], ci[i][1]),
-                           mx_scale_clamp(v[2], ci[i][2]), mx_scale_clamp(v[3], ci[i][3]));
+          pk = e4m3x4_of_bf16(v[0], v[1], v[2], v[3], osc[i], 448.0f * osc[i]);  // rounds to BF16 first
         }
         __builtin_amdgcn_raw_buffer_store_b32(pk, rsrc, (int)off, 0, 0);
       }
@@ -276,7 +274,7 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
 template <int KIND, int OUT, int POOL, int MB, int NB>
 __device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc_i)[NB][MB], const v4f (&acc_f)[NB][MB],
                                               int row0, int n_tile0, int nl0, const float* ep_scale,
-                                              const float* ep_bias, const float* ep_oinv) {
+                                              const float* ep_bias, const float* ep_osc) {
   // a residual in the output's own dense BF16 layout (the refiner blocks' contract convs) stays on the fast path
   const bool res_dense = a.residual != nullptr && a.res_dtype == FIM_BF16 && a.res_channels == a.Cout && a.rs_c == 1 &&
                          a.rs_w == a.Cout && a.rs_h == (int64_t)a.Wo * a.Cout &&
@@ -287,14 +285,14 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc
     if (a.residual != nullptr) {
       if (a.gelu)
         conv_epilogue_fast<KIND, OUT, MB, NB, true, true>(a, acc_i, acc_f, row0, n_tile0, nl0, ep_scale, ep_bias,
-                                                          ep_oinv);
+                                                          ep_osc);
       else
         conv_epilogue_fast<KIND, OUT, MB, NB, false, true>(a, acc_i, acc_f, row0, n_tile0, nl0, ep_scale, ep_bias,
-                                                           ep_oinv);
+                                                           ep_osc);
     } else if (a.gelu) {
-      conv_epilogue_fast<KIND, OUT, MB, NB, true>(a, acc_i, acc_f, row0, n_tile0, nl0, ep_scale, ep_bias, ep_oinv);
+      conv_epilogue_fast<KIND, OUT, MB, NB, true>(a, acc_i, acc_f, row0, n_tile0, nl0, ep_scale, ep_bias, ep_osc);
     } else {
-      conv_epilogue_fast<KIND, OUT, MB, NB, false>(a, acc_i, acc_f, row0, n_tile0, nl0, ep_scale, ep_bias, ep_oinv);
+      conv_epilogue_fast<KIND, OUT, MB, NB, false>(a, acc_i, acc_f, row0, n_tile0, nl0, ep_scale, ep_bias, ep_osc);
     }
     return;
   }
@@ -327,10 +325,9 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc
     const int nbase = n_tile0 + nl;
     const float4 cs4 = *reinterpret_cast<const float4*>(&ep_scale[nl]);
     const float4 cb4 = *reinterpret_cast<const float4*>(&ep_bias[nl]);
-    const float4 ci4 = *reinterpret_cast<const float4*>(&ep_oinv[nl]);
+    const float osc = ep_osc[nl];  // E4M3 output scale of the lane's 4 channels (one 32-channel block)
     const float cs[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
     const float cb[4] = {cb4.x, cb4.y, cb4.z, cb4.w};
-    const float ci[4] = {ci4.x, ci4.y, ci4.z, ci4.w};
     const bool full = nbase + 4 <= a.Cout;
     const bool any = nbase < a.Cout;
     const bool res_full = res_vec && nbase + 4 <= a.res_channels;
@@ -443,8 +440,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc
 #pragma unroll
           for (int v = 0; v < 4; ++v) pk |= (uint32_t)(uint8_t)quantize_int8_fast(y[v], out_scale, out_inv) << (8 * v);
         } else {
-          pk = pack_e4m3x4(mx_scale_clamp(y[0], ci[0]), mx_scale_clamp(y[1], ci[1]), mx_scale_clamp(y[2], ci[2]),
-                           mx_scale_clamp(y[3], ci[3]));
+          pk = e4m3x4_of_bf16(y[0], y[1], y[2], y[3], osc, 448.0f * osc);
         }
         uint8_t* dst = static_cast<uint8_t*>(a.out) + o;
         if (out_vec && full) {
@@ -469,7 +465,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
   constexpr int B_PASSES = BN / 32;
   constexpr int STAGE = (BM + BN) * KC;  // pixel rows first, then weight rows; 128 B per row, XOR-swizzled
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
-  __shared__ __attribute__((aligned(16))) float ep_scale[BN], ep_bias[BN], ep_oinv[BN];  // per-channel epilogue operands of this N tile
+  __shared__ __attribute__((aligned(16))) float ep_scale[BN], ep_bias[BN], ep_osc[BN];  // per-channel epilogue operands of this N tile
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -497,7 +493,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
       bias = a.bias_dtype == FIM_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(a.bias)[n])
                                       : static_cast<const float*>(a.bias)[n];
     ep_bias[tid] = bias;
-    ep_oinv[tid] = (OUT == OUT_E4M3 && nok) ? exp2_int(-(int)a.out_expo[n >> 5]) : 1.0f;
+    ep_osc[tid] = (OUT == OUT_E4M3 && nok) ? exp2_int((int)a.out_expo[n >> 5]) : 1.0f;  // E4M3 output scale 2^e
   }
 
   const int seg = tid & 7;    // 16-byte segment of the 128-byte K chunk this lane stages
@@ -751,7 +747,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
   }
 
   FIM_STAMP(2);
-  conv_epilogue<KIND, OUT, POOL, MB, NB>(a, acc_i, acc_f, m0 + wm * (MB * 16), n0, wn * (BN / 2), ep_scale, ep_bias, ep_oinv);
+  conv_epilogue<KIND, OUT, POOL, MB, NB>(a, acc_i, acc_f, m0 + wm * (MB * 16), n0, wn * (BN / 2), ep_scale, ep_bias, ep_osc);
   FIM_STAMP(3);
 }
 
@@ -788,7 +784,7 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
   __shared__ __attribute__((aligned(16))) uint8_t st0[STAGE];
   __shared__ __attribute__((aligned(16))) uint8_t st1[STAGE];
   __shared__ __attribute__((aligned(16))) uint8_t st2[NST == 3 ? STAGE : 16];
-  __shared__ __attribute__((aligned(16))) float ep_scale[BN], ep_bias[BN], ep_oinv[BN];
+  __shared__ __attribute__((aligned(16))) float ep_scale[BN], ep_bias[BN], ep_osc[BN];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -815,7 +811,7 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
       bias = a.bias_dtype == FIM_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(a.bias)[n])
                                       : static_cast<const float*>(a.bias)[n];
     ep_bias[tid] = bias;
-    ep_oinv[tid] = (OUT == OUT_E4M3 && nok) ? exp2_int(-(int)a.out_expo[n >> 5]) : 1.0f;
+    ep_osc[tid] = (OUT == OUT_E4M3 && nok) ? exp2_int((int)a.out_expo[n >> 5]) : 1.0f;  // E4M3 output scale 2^e
   }
 
   const int wrow = a.kh * a.kw * a.Cin;  // < 2^31: the host bounds the weight bytes
@@ -1041,7 +1037,7 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
 
   FIM_STAMP(2);
   conv_epilogue<KIND, OUT, 0, MB, NB>(a, acc_i, acc_f, m0 + wm * (MB * 16), n0, wn * (NB * 16), ep_scale, ep_bias,
-                                      ep_oinv);
+                                      ep_osc);
   FIM_STAMP(3);
 }
 

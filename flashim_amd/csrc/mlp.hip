@@ -60,7 +60,7 @@ __global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t w2s[MLP_C * MLP_H];  // [c][256 B]
   __shared__ __attribute__((aligned(16))) uint8_t xs[MLP_BM * MLP_C];  // [px][64 B]
   __shared__ __attribute__((aligned(16))) uint8_t hs[MLP_BM * MLP_H];  // [px][256 B]
-  __shared__ float b1s[MLP_H], b2s[MLP_C], s1[MLP_H], s2[MLP_C], hinv[MLP_H];
+  __shared__ float b1s[MLP_H], b2s[MLP_C], s1[MLP_H], s2[MLP_C], hsc[MLP_H];  // hsc: MX hidden scale 2^e
   __shared__ int8_t e1s[MLP_H * (MLP_C / 32)], e2s[MLP_C * (MLP_H / 32)];
 
   const int tid = threadIdx.x;
@@ -86,7 +86,7 @@ __global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
     if (KIND == MLP_INT8) {
       s1[h] = *static_cast<const float*>(a.x_scale) * static_cast<const float*>(a.w1_scale)[h];
     } else {
-      hinv[h] = exp2_int(-(int)static_cast<const int8_t*>(a.h_scale)[h >> 5]);
+      hsc[h] = exp2_int((int)static_cast<const int8_t*>(a.h_scale)[h >> 5]);
       e1s[2 * h] = static_cast<const int8_t*>(a.w1_scale)[2 * h];
       e1s[2 * h + 1] = static_cast<const int8_t*>(a.w1_scale)[2 * h + 1];
     }
@@ -208,20 +208,21 @@ __global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
             round_bf16x2(y[0], y[1]);
             round_bf16x2(y[2], y[3]);
           }
-#ifndef FIM_EXP_NOGELU
-#pragma unroll
-          for (int v = 0; v < 4; ++v) y[v] = gelu_erf(y[v]);
-#endif
-          round_bf16x2(y[0], y[1]);
-          round_bf16x2(y[2], y[3]);
         }
+#ifndef FIM_EXP_NOGELU
+        gelu_erf_n<16>(reinterpret_cast<float (&)[16]>(yb));  // the block's 16 GELU chains interleaved
+#endif
         uint32_t qw[4];
-        if (KIND == MLP_MX) {
+        if (KIND == MLP_MX) {  // BF16 rounding and static E4M3 in one step (the lane's 4 channels share a scale block)
+          const float sc = hsc[h0], bound = 448.0f * sc;
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            qw[j] = pack_e4m3x4(mx_scale_clamp(yb[j][0], hinv[h0]), mx_scale_clamp(yb[j][1], hinv[h0 + 1]),
-                                mx_scale_clamp(yb[j][2], hinv[h0 + 2]), mx_scale_clamp(yb[j][3], hinv[h0 + 3]));
+          for (int j = 0; j < 4; ++j) qw[j] = e4m3x4_of_bf16(yb[j][0], yb[j][1], yb[j][2], yb[j][3], sc, bound);
         } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            round_bf16x2(yb[j][0], yb[j][1]);
+            round_bf16x2(yb[j][2], yb[j][3]);
+          }
           const float (&flat)[16] = reinterpret_cast<const float (&)[16]>(yb);
           int qi[16];
           quantize_int8_fast_n<16>(flat, hq_scale, hq_inv, qi);
