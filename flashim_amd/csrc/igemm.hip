@@ -455,8 +455,12 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc
   }
 }
 
-template <int KIND, int BN, int LW, int OUT, int XS, int POOL, int MBW = 4, bool PACK = false>
-__global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
+// ONE: the launch has a single K step (K <= 128): one LDS stage and one register set (127-146 VGPRs instead of 254),
+// so three workgroups fit on a CU instead of two and more tiles' loads overlap the others' epilogues (refiner stack
+// MXFP8 20.4 -> 19.9 ms). A single-stage loop over several K steps keeps the next step's registers live through the
+// MFMAs and spills at the three-workgroup register budget.
+template <int KIND, int BN, int LW, int OUT, int XS, int POOL, int MBW = 4, bool PACK = false, bool ONE = false>
+__global__ __launch_bounds__(256, ONE ? 3 : 2) void conv_igemm_kernel(const ConvArgs a) {
   constexpr int MB = MBW;                // 16-pixel blocks per wavefront (64 pixels; 32 in the tail's small tiles)
   constexpr int BM = 32 * MB;            // pixel rows per tile: two wavefronts of MB blocks
   constexpr int SXN = XS ? MB : 1;       // activation scale registers per set: one per 16-pixel block with row scales
@@ -464,7 +468,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
   constexpr int A_PASSES = BM / 32;      // 256 lanes x 16 B cover 32 rows x 128 B per pass
   constexpr int B_PASSES = BN / 32;
   constexpr int STAGE = (BM + BN) * KC;  // pixel rows first, then weight rows; 128 B per row, XOR-swizzled
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[(ONE ? 1 : 2) * STAGE];
   __shared__ __attribute__((aligned(16))) float ep_scale[BN], ep_bias[BN], ep_osc[BN];  // per-channel epilogue operands of this N tile
 
   const int tid = threadIdx.x;
@@ -653,7 +657,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
 
   const int nk = PACK ? (a.kh * a.kw + a.tps - 1) / a.tps : a.kh * a.kw * a.kchunks;
   gload(ra0, rb0, sx0, sw0, bok0);
-  if (nk > 1) gload(ra1, rb1, sx1, sw1, bok1);
+  if (!ONE && nk > 1) gload(ra1, rb1, sx1, sw1, bok1);
   sstore(0, ra0, rb0);
   lds_barrier();
   FIM_STAMP(1);
@@ -707,6 +711,9 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(const ConvArgs a) {
     }
   };
 
+  if constexpr (ONE) {
+    compute(0, sx0, sw0, bok0);
+  } else
   // steps alternate register sets: even steps were loaded into set 0, odd steps into set 1
   for (int kt = 0; kt < nk; kt += 2) {
     // even step kt (LDS stage 0, scales in set 0); set 0 is free once staged: load step kt + 2 into it
@@ -1075,6 +1082,12 @@ static void launch_tail(const ConvArgs& a, int lw, dim3 grid, hipStream_t stream
 
 template <int KIND, int BN, int OUT, int XS, int POOL = 0>
 static void launch_lw(const ConvArgs& a, int lw, dim3 grid, hipStream_t stream) {
+  if constexpr (XS == 0 && POOL == 0) {
+    if (lw == 16 && a.kh * a.kw * a.kchunks == 1) {
+      conv_igemm_kernel<KIND, BN, 16, OUT, 0, 0, 4, false, true><<<grid, dim3(256), 0, stream>>>(a);
+      return;
+    }
+  }
   if (lw == 16)
     conv_igemm_kernel<KIND, BN, 16, OUT, XS, POOL><<<grid, dim3(256), 0, stream>>>(a);
   else

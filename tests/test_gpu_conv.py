@@ -386,3 +386,32 @@ def test_dense_residual_fast_epilogue(kind, gelu, wide):
         out_exponent = torch.randint(-3, 2, (cout // 32,), dtype=torch.int8)
         got_q = run(relu=True, residual=r.to(DEV), out_exponent=out_exponent.to(DEV))
         assert torch.equal(got_q.view(torch.uint8), ref.quantize_static(got, out_exponent).view(torch.uint8))
+
+
+@pytest.mark.parametrize("kind", ["int8", "mxfp8"])
+def test_single_k_step_kernel_quantized_outputs(kind):
+    """1x1 convs with K = 128 over many rounds run the single-K-step 128-row kernel (one LDS stage, three workgroups
+    per CU): INT8 bit-exact with the oracle (BF16 and INT8 out), MXFP8 at the oracle bar and its E4M3 output equal to
+    the BF16 output quantized separately."""
+    torch.manual_seed(41)
+    shape, geo = (1, 300, 256), (1, 1, 1, 1, 0, 0, 1, 1)
+    if kind == "int8":
+        x, w, a_scale, w_scale, bias = _int8_inputs(128, 128, 1, 1, True, shape=shape)
+        args = _dev(x, w, a_scale, w_scale, bias)
+        out_scale = torch.tensor(0.04)
+        got = ops.int8_conv2d.get("hip")(*args, *geo, relu=True).cpu()
+        assert torch.equal(got, ref.int8_conv2d(x, w, a_scale, w_scale, bias, *geo, relu=True))
+        got_q = ops.int8_conv2d.get("hip")(*args, *geo, relu=True, out_scale=out_scale.to(DEV)).cpu()
+        assert torch.equal(got_q, ref.int8_conv2d(x, w, a_scale, w_scale, bias, *geo, relu=True, out_scale=out_scale))
+    else:
+        x = (torch.randn(*shape, 128) * 3).to(torch.float8_e4m3fn)
+        ce = torch.randint(-6, 3, (4,), dtype=torch.int8)
+        w = (torch.randn(128, 128) * 2).to(torch.float8_e4m3fn)
+        we = torch.randint(-9, -3, (128, 4), dtype=torch.int8)
+        bias = torch.randn(128).to(torch.bfloat16)
+        run = lambda **k: ops.mxfp8_conv2d.get("hip")(*_dev(x, ce, w, we, bias), *geo, relu=True, **k).cpu()  # noqa: E731
+        got = run()
+        _assert_mx_close(got, ref.mxfp8_conv2d(x, ce, w, we, bias, *geo, relu=True))
+        out_exponent = torch.tensor([-2, -1, 0, 1], dtype=torch.int8)
+        got_q = run(out_exponent=out_exponent.to(DEV))
+        assert torch.equal(got_q.view(torch.uint8), ref.quantize_static(got, out_exponent).view(torch.uint8))
