@@ -7,6 +7,9 @@
   MXFP8 out) -> ``fim_depthwise5x5``
 * ``conv2d_small_cin_quantize_int8`` (``flashim/ops/conv.py:225-235``) -> ``fim_conv3x3_small_cin_quantize_int8``
 * ``bias_relu_quantize_int8`` (``flashim/ops/quantize.py:134-142``) -> ``fim_bias_relu_quantize_int8``
+* ``depthwise5x5_relu_pointwise_mxfp8`` / ``_int8`` (``flashim/ops/conv.py:93-138``) -> at C = 128 with a 128 x 128
+  pointwise weight ``fim_depthwise5x5_relu_pointwise_{mxfp8,int8}`` (one kernel, the reference's fused shapes
+  ``flashim/backends/triton/conv.py:310-508``), else the producer then ``fim_mxfp8_scaled_mm`` / ``fim_int8_linear``
 
 ``gelu=`` on the two convs is an epilogue FlashIM's conv ops do not have: it is ``int8_linear``'s GELU
 (``flashim/ops/gemm.py:94-95``): ``F.gelu`` of the BF16 result, rounded to BF16, before the residual.
