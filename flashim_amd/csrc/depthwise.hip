@@ -31,10 +31,12 @@ struct DwArgs {
   uint8_t* swizzled;       // MX dynamic scales (cuBLAS 128x4 layout), may be null
   int8_t* expo_out;        // MX dynamic exponents [rows, C / 32], may be null
   int B, H, W, C;
+  int tiles_x, tiles_y;    // column and row tiles per image
+  int64_t ntiles;          // tiles_x * tiles_y * B * (C / 32)
 };
 
-// Tile: 32 output columns x 16 output rows x 32 channels per workgroup (grid: column tiles, row tiles, batch x
-// 32-channel slices), with the 2-pixel halo of the 5x5 window staged in LDS once.
+// Tile: 32 output columns x 16 output rows x 32 channels per workgroup (a 1-D grid over (channel slice, column tile,
+// row tile, image), XCD-aware), with the 2-pixel halo of the 5x5 window staged in LDS once.
 constexpr int DW_TW = 32, DW_TH = 16, DW_CS = 32;  // output columns, output rows, channels per workgroup
 
 // ---- The taps on the matrix unit ----------------------------------------------------------------------------
@@ -60,11 +62,19 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t sm[DWM_LDS];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int x0 = blockIdx.x * DW_TW;
-  const int y0 = blockIdx.y * DW_TH;
+  // XCD-aware tile order: workgroup p runs on XCD p % 8, so each XCD takes a contiguous run of tiles in (channel slice,
+  // column tile, row tile, image) order, slice fastest: the slices of a pixel (which share its 128-byte input lines)
+  // and neighbouring column tiles (which share halo columns) read through the same L2 at about the same time.
+  // (One workgroup per tile in a 3-D grid read each input line from HBM about three times.)
   const int cslices = a.C / DW_CS;
-  const int b = blockIdx.z / cslices;
-  const int cbase = (blockIdx.z % cslices) * DW_CS;
+  const int64_t L = (int64_t)(blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+  if (L >= a.ntiles) return;
+  const int cbase = (int)(L % cslices) * DW_CS;
+  int64_t rest = L / cslices;
+  const int x0 = (int)(rest % a.tiles_x) * DW_TW;
+  rest /= a.tiles_x;
+  const int y0 = (int)(rest % a.tiles_y) * DW_TH;
+  const int b = (int)(rest / a.tiles_y);
 
   // stage: unit (row r, 4-column group q, channel octet o): 4 pixels x 8 channels, transposed (v_perm) into 8
   // channel rows of 4 BF16, one 8-byte LDS write each; loads unconditional from clamped in-image addresses
@@ -301,11 +311,12 @@ int fim_depthwise5x5(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t
   if (B * H * W == 0) return FIM_OK;
   if (H > 2147483647LL || W > 2147483647LL) return FIM_ERR_UNSUPPORTED;
   if (((uintptr_t)x % 16) != 0) return FIM_ERR_UNSUPPORTED;
-  DwArgs a{x, weight, bias, scale, exponent, out, swizzled, exponent_out, (int)B, (int)H, (int)W, (int)C};
-  const int64_t gz = B * (C / DW_CS);
-  const int64_t gy = cdiv(H, DW_TH);
-  if (gz > 65535 || gy > 65535) return FIM_ERR_UNSUPPORTED;
-  dim3 grid((unsigned)cdiv(W, DW_TW), (unsigned)gy, (unsigned)gz);
+  const int64_t tx = cdiv(W, DW_TW), ty = cdiv(H, DW_TH);
+  const int64_t ntiles = tx * ty * B * (C / DW_CS);
+  if (ntiles > (1LL << 31) - 8) return FIM_ERR_UNSUPPORTED;
+  DwArgs a{x, weight, bias, scale, exponent, out, swizzled, exponent_out, (int)B, (int)H, (int)W, (int)C,
+           (int)tx, (int)ty, ntiles};
+  dim3 grid((unsigned)(cdiv(ntiles, 8) * 8));  // a multiple of the 8 XCDs: the kernel maps pids to tiles per XCD
   if (act == ACT_RELU)
     dw_launch_out<ACT_RELU>(a, out_mode, grid, stream);
   else
