@@ -7,9 +7,11 @@
   MXFP8 out) -> ``fim_depthwise5x5``
 * ``conv2d_small_cin_quantize_int8`` (``flashim/ops/conv.py:225-235``) -> ``fim_conv3x3_small_cin_quantize_int8``
 * ``bias_relu_quantize_int8`` (``flashim/ops/quantize.py:134-142``) -> ``fim_bias_relu_quantize_int8``
-* ``depthwise5x5_relu_pointwise_mxfp8`` / ``_int8`` (``flashim/ops/conv.py:93-138``) -> at C = 128 with a 128 x 128
-  pointwise weight ``fim_depthwise5x5_relu_pointwise_{mxfp8,int8}`` (one kernel, the reference's fused shapes
-  ``flashim/backends/triton/conv.py:310-508``), else the producer then ``fim_mxfp8_scaled_mm`` / ``fim_int8_linear``
+* ``depthwise5x5_relu_pointwise_mxfp8`` (``flashim/ops/conv.py:93-113``) -> at C = 128 with a 128 x 128 pointwise
+  weight ``fim_depthwise5x5_relu_pointwise_mxfp8`` (one kernel, the reference's fused shapes
+  ``flashim/backends/triton/conv.py:310-508``), else the producer then ``fim_mxfp8_scaled_mm``
+* ``depthwise5x5_relu_pointwise_int8`` (``flashim/ops/conv.py:119-138``) -> the producer then ``fim_int8_linear`` (the
+  measured faster of the two; ``fim_depthwise5x5_relu_pointwise_int8`` is ``pointwise_int8_fused``, same bits)
 
 ``gelu=`` on the two convs is an epilogue FlashIM's conv ops do not have: it is ``int8_linear``'s GELU
 (``flashim/ops/gemm.py:94-95``): ``F.gelu`` of the BF16 result, rounded to BF16, before the residual.
@@ -300,10 +302,19 @@ def pointwise_mxfp8_composite(value: Tensor, dw_weight: Tensor, dw_bias: Tensor,
 
 def depthwise5x5_relu_pointwise_int8(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
                                      pw_wscale: Tensor, pw_bias: Tensor, scale: Tensor) -> Tensor:
-    """The INT8 refiner block (``flashim/ops/conv.py:119-138``) -> ``[B, C, H, W]`` view of NHWC BF16. At 128 x 128
-    one kernel (``fim_depthwise5x5_relu_pointwise_int8``), else the composite."""
+    """The INT8 refiner block (``flashim/ops/conv.py:119-138``) -> ``[B, C, H, W]`` view of NHWC BF16: the two-launch
+    composite at every shape. Its INT8 intermediate is 1 byte per element, and on MI355X at 2 x 128 x 400 x 400 the
+    composite measures 84 us against 90 us for the one-kernel ``pointwise_int8_fused``, which gives the same bits."""
+    return pointwise_int8_composite(value, dw_weight, dw_bias, pw_weight, pw_wscale, pw_bias, scale)
+
+
+def pointwise_int8_fused(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor, pw_wscale: Tensor,
+                         pw_bias: Tensor, scale: Tensor) -> Tensor:
+    """One kernel (``fim_depthwise5x5_relu_pointwise_int8``) at C = 128 with a 128 x 128 pointwise weight; bit for bit
+    the composite."""
     if not _fused_pointwise_shape(value, pw_weight):
-        return pointwise_int8_composite(value, dw_weight, dw_bias, pw_weight, pw_wscale, pw_bias, scale)
+        raise ValueError(f"pointwise_int8_fused needs C = 128 and a 128 x 128 weight, got {tuple(value.shape)}, "
+                         f"{tuple(pw_weight.shape)}")
     from flashim_amd.backends.hip import gemm
 
     batch, channels, height, width = value.shape

@@ -42,6 +42,8 @@ struct DwPwArgs {
   int pw_b_dtype;
   uint16_t* out;            // BF16 [B, H, W, 128]
   int B, H, W;
+  int tiles_x, tiles_y;
+  int64_t ntiles;           // tiles_x * tiles_y * B
 };
 
 typedef __bf16 v4bf16 __attribute__((ext_vector_type(4)));
@@ -57,7 +59,13 @@ __global__ __launch_bounds__(256, 2) void dw_pw_kernel(const DwPwArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int x0 = blockIdx.x * DP_TW, y0 = blockIdx.y * DP_TH, b = blockIdx.z;
+  // XCD-aware tile order (workgroup p runs on XCD p % 8): each XCD takes a contiguous run of tiles, column tiles
+  // fastest, so a tile's row neighbours, which share 4 of its 12 input rows, read through the same L2 shortly after
+  const int64_t L = (int64_t)(blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+  if (L >= a.ntiles) return;
+  const int x0 = (int)(L % a.tiles_x) * DP_TW;
+  const int y0 = (int)((L / a.tiles_x) % a.tiles_y) * DP_TH;
+  const int b = (int)(L / ((int64_t)a.tiles_x * a.tiles_y));
   const int rows = min(DP_TH, a.H - y0), cols = min(DP_TW, a.W - x0);
 
   // pointwise weight and per-channel operands, staged once (swizzle: 16-byte slot s of row n at s ^ ((n >> 1) & 7))
@@ -283,13 +291,16 @@ static int dwpw_launch(const DwPwArgs& a, int kind, int64_t C, int64_t N, hipStr
       ((uintptr_t)a.dw_w % 2) != 0)
     return FIM_ERR_UNSUPPORTED;
   if ((int64_t)a.B * a.H * a.W == 0) return FIM_OK;
-  const int64_t gx = cdiv(a.W, DP_TW), gy = cdiv(a.H, DP_TH);
-  if (gy > 65535 || a.B > 65535 || gx > 2147483647LL) return FIM_ERR_UNSUPPORTED;
-  const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)a.B);
+  DwPwArgs t = a;
+  t.tiles_x = (int)cdiv(a.W, DP_TW);
+  t.tiles_y = (int)cdiv(a.H, DP_TH);
+  t.ntiles = (int64_t)t.tiles_x * t.tiles_y * a.B;
+  if (t.ntiles > (1LL << 31) - 8) return FIM_ERR_UNSUPPORTED;
+  const dim3 grid((unsigned)(cdiv(t.ntiles, 8) * 8));  // a multiple of the 8 XCDs
   if (kind == DP_MX)
-    dw_pw_kernel<DP_MX><<<grid, dim3(256), 0, stream>>>(a);
+    dw_pw_kernel<DP_MX><<<grid, dim3(256), 0, stream>>>(t);
   else
-    dw_pw_kernel<DP_INT8><<<grid, dim3(256), 0, stream>>>(a);
+    dw_pw_kernel<DP_INT8><<<grid, dim3(256), 0, stream>>>(t);
   return launch_status();
 }
 
@@ -303,7 +314,7 @@ int fim_depthwise5x5_relu_pointwise_mxfp8(const uint16_t* x, int64_t B, int64_t 
   if (B > 2147483647LL || H > 2147483647LL || W > 2147483647LL || B * H * W * C >= (1LL << 40))
     return FIM_ERR_UNSUPPORTED;
   DwPwArgs a{x, dw_weight, dw_bias, pw_weight, pw_scale_e8m0, nullptr, nullptr, pw_bias, pw_bias_dtype, out,
-             (int)B, (int)H, (int)W};
+             (int)B, (int)H, (int)W, 0, 0, 0};
   return dwpw_launch(a, DP_MX, C, N, stream);
 }
 
@@ -315,7 +326,7 @@ int fim_depthwise5x5_relu_pointwise_int8(const uint16_t* x, int64_t B, int64_t H
   if (B > 2147483647LL || H > 2147483647LL || W > 2147483647LL || B * H * W * C >= (1LL << 40))
     return FIM_ERR_UNSUPPORTED;
   DwPwArgs a{x, dw_weight, dw_bias, reinterpret_cast<const uint8_t*>(pw_weight), nullptr, pw_wscale, a_scale, pw_bias,
-             pw_bias_dtype, out, (int)B, (int)H, (int)W};
+             pw_bias_dtype, out, (int)B, (int)H, (int)W, 0, 0, 0};
   return dwpw_launch(a, DP_INT8, C, N, stream);
 }
 

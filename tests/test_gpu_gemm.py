@@ -212,6 +212,6 @@ def test_fused_depthwise_pointwise_matches_composite(batch, hw, bias):
     pw_w8 = torch.randint(-127, 128, (channels, channels), dtype=torch.int8, generator=g)
     pw_s = torch.rand(channels, generator=g) * 0.01 + 0.001
     args = dev((x, dw_w, dw_b, pw_w8, pw_s, pw_b, torch.tensor(0.03)))
-    fused = ops.depthwise5x5_relu_pointwise_int8.get("hip")(*args)
-    composite = hip_conv.pointwise_int8_composite(*args)
+    fused = hip_conv.pointwise_int8_fused(*args)
+    composite = ops.depthwise5x5_relu_pointwise_int8.get("hip")(*args)
     assert torch.equal(fused.view(torch.int16), composite.view(torch.int16))
