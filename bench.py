@@ -79,8 +79,9 @@ def time_graph(fn, steps: int, warmup: int, per_graph: int = 10) -> float:
     return start.elapsed_time(end) / (replays * per_graph)
 
 
-def time_cpu(fn, budget_s: float = 10.0, max_calls: int = 50, warmup: int = 2) -> tuple[float, int]:
-    """Median ms of ``fn`` over up to ``max_calls`` calls within ``budget_s`` seconds (after ``warmup`` calls)."""
+def time_cpu(fn, budget_s: float = 10.0, max_calls: int = 2000, warmup: int = 2) -> tuple[float, int]:
+    """Median ms of ``fn`` over the calls that fit in ``budget_s`` seconds (at most ``max_calls``; after ``warmup``
+    calls), so the sample is a bounded ~10 s of CPU work whatever the host's speed."""
     for _ in range(warmup):
         fn()
     samples = []
@@ -238,7 +239,7 @@ def cpu_baseline_cfg2(args, steps_budget_s: float = 10.0) -> dict:
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import reference as ref
 
-    cores = os.cpu_count() or 1
+    cores = min(os.cpu_count() or 1, 16)  # the GPU box's CPU share is 16 threads, whatever os.cpu_count() reports
     torch.set_num_threads(cores)
     cpu_args = [a.cpu() if isinstance(a, torch.Tensor) else a for a in args]
     ms, calls = time_cpu(lambda: ref.mxfp8_conv2d(*cpu_args, gelu=True), budget_s=steps_budget_s)
@@ -247,7 +248,8 @@ def cpu_baseline_cfg2(args, steps_budget_s: float = 10.0) -> dict:
         "value": round(ops / (ms * 1e-3) / 1e12, 5), "unit": "TOPS", "cores": cores, "kind": "port",
         "ms": round(ms, 3),
         "sample": f"config 2 in full (M=20000, K=N=512, bias+GELU): oracle.reference.mxfp8_conv2d (torch CPU, "
-                  f"FlashIM's reference path restated), median of {calls} calls, torch threads={cores}",
+                  f"FlashIM's reference path restated), median of {calls} calls "
+                  f"(~{calls * ms / 1e3:.1f} s of CPU work), torch threads={cores}",
     }
 
 
