@@ -28,6 +28,8 @@ SIGNATURES: dict[str, list] = {
     "fim_version": [],
     "fim_quantize_int8": [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp],
     "fim_quantize_mxfp8": [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp],
+    "fim_gelu_quantize_mxfp8": [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp],
+    "fim_gelu_quantize_int8": [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp],
     "fim_quantize_mxfp8_dynamic": [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp],
     "fim_quantize_int8_rows": [_vp, _i32, _i64, _i64, _i64, _i32, _vp, _vp, _vp],
     "fim_calibrate_block32": [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp],
@@ -46,6 +48,7 @@ SIGNATURES: dict[str, list] = {
     "fim_int8_linear": [
         _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _i64, _i64, _vp, _vp, _vp,
     ],
+    "fim_int8_linear_quantize": [_vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _vp],
     "fim_mxfp8_scaled_mm": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i32, _vp, _vp],
     "fim_im2col_gather": [_vp, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp],
     "fim_refiner_mlp": [_i32, _i32, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _vp,

@@ -19,40 +19,48 @@
 
 from __future__ import annotations
 
-import ctypes
-
 import torch
 from torch import Tensor
 
-from flashim_amd import _lib, quant
+from flashim_amd import library, quant
 from flashim_amd.platforms import is_gfx950
 
 
-def conv_output_size(h: int, w: int, kh: int, kw: int, sh: int, sw: int, ph: int, pw: int, dh: int, dw: int):
-    return (h + 2 * ph - dh * (kh - 1) - 1) // sh + 1, (w + 2 * pw - dw * (kw - 1) - 1) // sw + 1
+conv_output_size = library.conv_out_hw
 
 
-def _bias_args(bias: Tensor | None, device: torch.device) -> tuple[Tensor | None, int]:
+def _bias(bias: Tensor | None, device: torch.device) -> Tensor | None:
+    """FP32 or BF16 ``[N]`` on ``device`` (other dtypes promoted to FP32), or ``None``."""
     if bias is None:
-        return None, 0
+        return None
     if bias.dtype not in (torch.float32, torch.bfloat16):
         bias = bias.float()
-    bias = bias.to(device).contiguous()
-    return bias, 1 if bias.dtype == torch.bfloat16 else 0
+    return bias.to(device).contiguous()
 
 
-def _residual_args(residual: Tensor | None, device: torch.device, out_shape: tuple[int, int, int, int]):
-    """(tensor, dtype code, channels, ctypes int64[4] strides); the kernel reads ``[B, Ho, Wo, <= Cout]``."""
+def _residual(residual: Tensor | None, device: torch.device, out_shape: tuple[int, int, int, int]) -> Tensor | None:
+    """The residual as the kernels read it: ``[B, Ho, Wo, <= Cout]`` FP32 or BF16, any strides."""
     if residual is None:
-        return None, 0, 0, None
+        return None
     if residual.ndim != 4 or tuple(residual.shape[:3]) != tuple(out_shape[:3]) or residual.shape[3] > out_shape[3]:
         raise ValueError(f"residual {tuple(residual.shape)} does not fit the output {tuple(out_shape)}")
     if residual.device != device:
         raise ValueError("residual must be on the output's device")
     if residual.dtype not in (torch.float32, torch.bfloat16):
         residual = residual.to(torch.bfloat16)
-    strides = (ctypes.c_int64 * 4)(*residual.stride())
-    return residual, _lib.DTYPE_CODES[residual.dtype], residual.shape[-1], strides
+    return residual
+
+
+def _scalar(t: Tensor, device) -> Tensor:
+    return t.to(device=device, dtype=torch.float32).reshape(1).contiguous()
+
+
+def _same_scale(scale: Tensor, device) -> Tensor:
+    """The caller's scale object itself when it is already one FP32 value on ``device``: FlashIM's layers recognise
+    an input quantized for them by the identity of its scale."""
+    if scale.dtype == torch.float32 and scale.numel() == 1 and scale.device == device:
+        return scale
+    return scale.to(device=device, dtype=torch.float32).reshape(())
 
 
 def int8_conv2d(
@@ -62,25 +70,14 @@ def int8_conv2d(
 ) -> Tensor:
     """``x`` int8 ``[B, H, W, Cin]`` (packed), ``weight`` int8 ``[Cout, kh*kw*Cin]`` (ky, kx, c) -> BF16
     ``[B, Ho, Wo, Cout]``, or int8 with ``out_scale``."""
-    b, h, w, cin = x.shape
+    b, h, w, _ = x.shape
     cout = weight.shape[0]
     ho, wo = conv_output_size(h, w, kh, kw, sh, sw, ph, pw, dh, dw)
-    x = x.contiguous()
-    weight = weight.contiguous()
-    a_scale = a_scale.to(device=x.device, dtype=torch.float32).reshape(1).contiguous()
-    w_scale = w_scale.to(device=x.device, dtype=torch.float32).contiguous()
-    bias, bias_code = _bias_args(bias, x.device)
-    res, res_code, res_channels, res_strides = _residual_args(residual, x.device, (b, ho, wo, cout))
-    if out_scale is not None:
-        out_scale = out_scale.to(device=x.device, dtype=torch.float32).reshape(1).contiguous()
-    out = torch.empty(b, ho, wo, cout, device=x.device, dtype=torch.int8 if out_scale is not None else torch.bfloat16)
-    _lib.call(
-        "fim_int8_conv2d", x.data_ptr(), b, h, w, cin, weight.data_ptr(), cout, a_scale.data_ptr(),
-        w_scale.data_ptr(), _lib.ptr(bias), bias_code, kh, kw, sh, sw, ph, pw, dh, dw, int(relu), int(gelu),
-        _lib.ptr(res), res_code, res_channels, res_strides, _lib.ptr(out_scale), out.data_ptr(), _lib.stream_of(x),
-        what=f"int8_conv2d {tuple(x.shape)} -> {cout} k{kh}x{kw}",
-    )
-    return out
+    return library.int8_conv2d(
+        x.contiguous(), weight.contiguous(), _scalar(a_scale, x.device),
+        w_scale.to(device=x.device, dtype=torch.float32).contiguous(), _bias(bias, x.device),
+        kh, kw, sh, sw, ph, pw, dh, dw, bool(relu), bool(gelu), _residual(residual, x.device, (b, ho, wo, cout)),
+        None if out_scale is None else _scalar(out_scale, x.device))
 
 
 def int8_conv2d_maxpool(
@@ -89,24 +86,10 @@ def int8_conv2d_maxpool(
 ) -> tuple[Tensor, Tensor]:
     """``(out, pooled)``: the BF16 ``[B, Ho, Wo, Cout]`` conv output and the INT8 ``[B, Ho/2, Wo/2, Cout]`` 2x2 max pool
     of it quantized with ``out_scale`` (``ops/conv.py:209-222``), the pool from the conv's epilogue."""
-    b, h, w, cin = x.shape
-    cout = weight.shape[0]
-    ho, wo = conv_output_size(h, w, kh, kw, sh, sw, ph, pw, dh, dw)
-    x = x.contiguous()
-    weight = weight.contiguous()
-    a_scale = a_scale.to(device=x.device, dtype=torch.float32).reshape(1).contiguous()
-    w_scale = w_scale.to(device=x.device, dtype=torch.float32).contiguous()
-    bias, bias_code = _bias_args(bias, x.device)
-    out_scale = out_scale.to(device=x.device, dtype=torch.float32).reshape(1).contiguous()
-    out = torch.empty(b, ho, wo, cout, device=x.device, dtype=torch.bfloat16)
-    pooled = torch.empty(b, ho // 2, wo // 2, cout, device=x.device, dtype=torch.int8)
-    _lib.call(
-        "fim_int8_conv2d_maxpool", x.data_ptr(), b, h, w, cin, weight.data_ptr(), cout, a_scale.data_ptr(),
-        w_scale.data_ptr(), _lib.ptr(bias), bias_code, kh, kw, sh, sw, ph, pw, dh, dw, int(relu), out_scale.data_ptr(),
-        out.data_ptr(), pooled.data_ptr(), _lib.stream_of(x),
-        what=f"int8_conv2d_maxpool {tuple(x.shape)} -> {cout} k{kh}x{kw}",
-    )
-    return out, pooled
+    return library.int8_conv2d_maxpool(
+        x.contiguous(), weight.contiguous(), _scalar(a_scale, x.device),
+        w_scale.to(device=x.device, dtype=torch.float32).contiguous(), _bias(bias, x.device),
+        kh, kw, sh, sw, ph, pw, dh, dw, bool(relu), _scalar(out_scale, x.device))
 
 
 def mxfp8_conv2d(
@@ -117,31 +100,20 @@ def mxfp8_conv2d(
     """``x`` E4M3 ``[B, H, W, Cin]`` (``Cin % 32 == 0``), ``channel_exponent`` int8 ``[Cin / 32]``, ``weight`` E4M3
     ``[Cout, kh*kw*Cin]`` with ``weight_exponent`` ``[Cout, kh*kw*Cin / 32]`` -> BF16 ``[B, Ho, Wo, Cout]``, or E4M3
     with ``out_exponent``."""
-    b, h, w, cin = x.shape
+    b, h, w, _ = x.shape
     cout = weight.shape[0]
     ho, wo = conv_output_size(h, w, kh, kw, sh, sw, ph, pw, dh, dw)
-    x = x.contiguous()
-    weight = weight.contiguous()
-    channel_exponent = channel_exponent.to(device=x.device, dtype=torch.int8).contiguous()
-    weight_exponent = weight_exponent.to(device=x.device, dtype=torch.int8).contiguous()
-    bias, bias_code = _bias_args(bias, x.device)
-    res, res_code, res_channels, res_strides = _residual_args(residual, x.device, (b, ho, wo, cout))
     if out_exponent is not None:
         out_exponent = out_exponent.to(device=x.device, dtype=torch.int8).contiguous()
-    out = torch.empty(b, ho, wo, cout, device=x.device,
-                      dtype=torch.float8_e4m3fn if out_exponent is not None else torch.bfloat16)
-    _lib.call(
-        "fim_mxfp8_conv2d", x.data_ptr(), b, h, w, cin, channel_exponent.data_ptr(), weight.data_ptr(), cout,
-        weight_exponent.data_ptr(), _lib.ptr(bias), bias_code, kh, kw, sh, sw, ph, pw, dh, dw, int(relu), int(gelu),
-        _lib.ptr(res), res_code, res_channels, res_strides, _lib.ptr(out_exponent), out.data_ptr(),
-        _lib.stream_of(x), what=f"mxfp8_conv2d {tuple(x.shape)} -> {cout} k{kh}x{kw}",
-    )
-    return out
+    out = library.mxfp8_conv2d(
+        x.contiguous().view(torch.uint8), channel_exponent.to(device=x.device, dtype=torch.int8).contiguous(),
+        weight.contiguous().view(torch.uint8), weight_exponent.to(device=x.device, dtype=torch.int8).contiguous(),
+        _bias(bias, x.device), kh, kw, sh, sw, ph, pw, dh, dw, bool(relu), bool(gelu),
+        _residual(residual, x.device, (b, ho, wo, cout)), out_exponent)
+    return out if out_exponent is None else out.view(torch.float8_e4m3fn)
 
 
 # -- depthwise 5x5 producers ------------------------------------------------------------------------------------
-
-_DW_MX_DYNAMIC, _DW_INT8, _DW_BF16, _DW_MX_STATIC = 0, 1, 2, 3
 
 
 def _nhwc_bf16(value: Tensor) -> Tensor:
@@ -152,39 +124,21 @@ def _nhwc_bf16(value: Tensor) -> Tensor:
     return value.permute(0, 2, 3, 1).contiguous()
 
 
-def _dw_launch(value: Tensor, weight: Tensor, bias: Tensor, act: int, mode: int, scale=None, exponent=None,
-               want_exponent: bool = False, want_swizzled: bool = False):
-    batch, channels, height, width = value.shape
-    x = _nhwc_bf16(value)
-    weight = weight.to(device=value.device, dtype=torch.bfloat16).contiguous()
-    bias = bias.to(device=value.device, dtype=torch.float32).contiguous()
-    rows = batch * height * width
-    out_dtype = {_DW_MX_DYNAMIC: torch.float8_e4m3fn, _DW_INT8: torch.int8, _DW_BF16: torch.bfloat16,
-                 _DW_MX_STATIC: torch.float8_e4m3fn}[mode]
-    out = torch.empty(rows, channels, device=value.device, dtype=out_dtype)
-    exponent_out = torch.empty(rows, channels // 32, device=value.device, dtype=torch.int8) if want_exponent else None
-    swizzled = quant.swizzled_buffer(rows, channels // 32, value.device) if want_swizzled else None
-    if scale is not None:
-        scale = scale.to(device=value.device, dtype=torch.float32).reshape(1).contiguous()
-    if exponent is not None:
-        exponent = exponent.to(device=value.device, dtype=torch.int8).contiguous()
-    _lib.call(
-        "fim_depthwise5x5", x.data_ptr(), batch, height, width, channels, weight.data_ptr(), bias.data_ptr(), act,
-        mode, _lib.ptr(scale), _lib.ptr(exponent), out.data_ptr(), _lib.ptr(exponent_out), _lib.ptr(swizzled),
-        _lib.stream_of(value), what=f"depthwise5x5 {tuple(value.shape)}",
-    )
-    return out, exponent_out, swizzled
+def _dw_operands(value: Tensor, weight: Tensor, bias: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    return (_nhwc_bf16(value), weight.to(device=value.device, dtype=torch.bfloat16).contiguous(),
+            bias.to(device=value.device, dtype=torch.float32).contiguous())
 
 
 def depthwise5x5_relu_mxfp8(value: Tensor, weight: Tensor, bias: Tensor) -> tuple[Tensor, Tensor]:
     """E4M3 ``[B*H*W, C]`` and the swizzled E8M0 scales of ``relu(dwconv5x5(value) + bias)``."""
-    out, _, swizzled = _dw_launch(value, weight, bias, 0, _DW_MX_DYNAMIC, want_swizzled=True)
-    return out, swizzled.view(torch.float8_e8m0fnu)
+    codes, swizzled = library.depthwise5x5_mx_dynamic(*_dw_operands(value, weight, bias))
+    return codes.view(torch.float8_e4m3fn), swizzled.view(torch.float8_e8m0fnu)
 
 
 def depthwise5x5_relu_int8(value: Tensor, weight: Tensor, bias: Tensor, scale: Tensor) -> Tensor:
     """int8 ``[B*H*W, C]``: ``relu(dwconv5x5(value) + bias)`` rounded to BF16, statically quantized."""
-    return _dw_launch(value, weight, bias, 0, _DW_INT8, scale=scale)[0]
+    return library.depthwise5x5(*_dw_operands(value, weight, bias), 0, library.DW_INT8, _scalar(scale, value.device),
+                                None)
 
 
 def depthwise5x5_gelu(value: Tensor, weight: Tensor, bias: Tensor, *, scale: Tensor | None = None,
@@ -193,8 +147,88 @@ def depthwise5x5_gelu(value: Tensor, weight: Tensor, bias: Tensor, *, scale: Ten
     statically quantized to INT8, with ``exponent`` (``[C/32]``) to E4M3."""
     if scale is not None and exponent is not None:
         raise ValueError("scale (INT8) and exponent (MXFP8) are exclusive")
-    mode = _DW_INT8 if scale is not None else _DW_MX_STATIC if exponent is not None else _DW_BF16
-    return _dw_launch(value, weight, bias, 1, mode, scale=scale, exponent=exponent)[0]
+    operands = _dw_operands(value, weight, bias)
+    if scale is not None:
+        return library.depthwise5x5(*operands, 1, library.DW_INT8, _scalar(scale, value.device), None)
+    if exponent is not None:
+        e = exponent.to(device=value.device, dtype=torch.int8).contiguous()
+        return library.depthwise5x5(*operands, 1, library.DW_MX_STATIC, None, e).view(torch.float8_e4m3fn)
+    return library.depthwise5x5(*operands, 1, library.DW_BF16, None, None)
+
+
+# -- im2col and the depthwise-then-pointwise composites ------------------------------------------------------------
+
+
+def im2col_gather(x: Tensor, kh: int, kw: int, sh: int, sw: int, ph: int, pw: int, dh: int, dw: int) -> Tensor:
+    """``x`` ``[B, H, W, C]`` of a 1-byte dtype -> ``[B*Ho*Wo, kh*kw*C]`` in (ky, kx, c) order, zero padding."""
+    return library.im2col_gather(x.contiguous().view(torch.uint8), kh, kw, sh, sw, ph, pw, dh, dw).view(x.dtype)
+
+
+def _fused_pointwise_shape(value: Tensor, pw_weight: Tensor) -> bool:
+    """The one-kernel block's shapes (``flashim/backends/triton/conv.py:561-599``): 128 channels in, 128 x 128
+    pointwise weight."""
+    return value.shape[1] == 128 and tuple(pw_weight.shape) == (128, 128)
+
+
+def depthwise5x5_relu_pointwise_mxfp8(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
+                                      pw_scale_swizzled: Tensor, pw_scale_u8: Tensor, pw_bias: Tensor) -> Tensor:
+    """The MXFP8 refiner block (``flashim/ops/conv.py:93-113``) -> ``[B, C, H, W]`` view of NHWC BF16. At 128 x 128
+    one kernel (``fim_depthwise5x5_relu_pointwise_mxfp8``: the quantized activations stay on chip), else the
+    composite."""
+    if not _fused_pointwise_shape(value, pw_weight):
+        return pointwise_mxfp8_composite(value, dw_weight, dw_bias, pw_weight, pw_scale_swizzled, pw_scale_u8,
+                                         pw_bias)
+    x, dw_w, dw_b = _dw_operands(value, dw_weight, dw_bias)
+    out = library.depthwise5x5_relu_pointwise_mxfp8(
+        x, dw_w, dw_b, pw_weight.contiguous().view(torch.uint8),
+        pw_scale_u8.to(value.device).contiguous().view(torch.uint8), _bias(pw_bias, value.device))
+    return out.permute(0, 3, 1, 2)
+
+
+def pointwise_mxfp8_composite(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
+                              pw_scale_swizzled: Tensor, pw_scale_u8: Tensor, pw_bias: Tensor) -> Tensor:
+    """Two launches: depthwise producer (dynamic MXFP8) then the block-scaled pointwise GEMM with the weight's plain
+    E8M0 bytes."""
+    batch, _, height, width = value.shape
+    codes, swizzled = library.depthwise5x5_mx_dynamic(*_dw_operands(value, dw_weight, dw_bias))
+    n, k = pw_weight.shape
+    w_exponent = (pw_scale_u8.view(torch.uint8).to(torch.int16) - 127).to(torch.int8).reshape(n, k // 32)
+    out = library.mxfp8_scaled_mm(codes, swizzled, pw_weight.contiguous().view(torch.uint8),
+                                  w_exponent.to(value.device).contiguous(), _bias(pw_bias, value.device))
+    return out.reshape(batch, height, width, n).permute(0, 3, 1, 2)
+
+
+def depthwise5x5_relu_pointwise_int8(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
+                                     pw_wscale: Tensor, pw_bias: Tensor, scale: Tensor) -> Tensor:
+    """The INT8 refiner block (``flashim/ops/conv.py:119-138``) -> ``[B, C, H, W]`` view of NHWC BF16: the two-launch
+    composite at every shape. Its INT8 intermediate is 1 byte per element, and on MI355X at 2 x 128 x 400 x 400 the
+    composite measures 84 us against 90 us for the one-kernel ``pointwise_int8_fused``, which gives the same bits."""
+    return pointwise_int8_composite(value, dw_weight, dw_bias, pw_weight, pw_wscale, pw_bias, scale)
+
+
+def pointwise_int8_fused(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor, pw_wscale: Tensor,
+                         pw_bias: Tensor, scale: Tensor) -> Tensor:
+    """One kernel (``fim_depthwise5x5_relu_pointwise_int8``) at C = 128 with a 128 x 128 pointwise weight; bit for bit
+    the composite."""
+    if not _fused_pointwise_shape(value, pw_weight):
+        raise ValueError(f"pointwise_int8_fused needs C = 128 and a 128 x 128 weight, got {tuple(value.shape)}, "
+                         f"{tuple(pw_weight.shape)}")
+    x, dw_w, dw_b = _dw_operands(value, dw_weight, dw_bias)
+    out = library.depthwise5x5_relu_pointwise_int8(
+        x, dw_w, dw_b, pw_weight.contiguous(), pw_wscale.to(device=value.device, dtype=torch.float32).reshape(-1)
+        .contiguous(), _scalar(scale, value.device), _bias(pw_bias, value.device))
+    return out.permute(0, 3, 1, 2)
+
+
+def pointwise_int8_composite(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
+                             pw_wscale: Tensor, pw_bias: Tensor, scale: Tensor) -> Tensor:
+    """Two launches: static INT8 producer then ``int8_linear``."""
+    from flashim_amd.backends.hip import gemm
+
+    batch, _, height, width = value.shape
+    quantized = depthwise5x5_relu_int8(value, dw_weight, dw_bias, scale)
+    out = gemm.int8_linear(quantized, pw_weight, scale, pw_wscale, pw_bias)
+    return out.reshape(batch, height, width, -1).permute(0, 3, 1, 2)
 
 
 # -- eligibility ----------------------------------------------------------------------------------------------------
@@ -237,112 +271,6 @@ def eligible_depthwise(value: Tensor, weight: Tensor, bias: Tensor, *rest, **kwa
     )
 
 
-# -- im2col and the depthwise-then-pointwise composites ------------------------------------------------------------
-
-
-def im2col_gather(x: Tensor, kh: int, kw: int, sh: int, sw: int, ph: int, pw: int, dh: int, dw: int) -> Tensor:
-    """``x`` ``[B, H, W, C]`` of a 1-byte dtype -> ``[B*Ho*Wo, kh*kw*C]`` in (ky, kx, c) order, zero padding."""
-    b, h, w, c = x.shape
-    ho, wo = conv_output_size(h, w, kh, kw, sh, sw, ph, pw, dh, dw)
-    x = x.contiguous()
-    out = torch.empty(b * ho * wo, kh * kw * c, device=x.device, dtype=x.dtype)
-    _lib.call("fim_im2col_gather", x.view(torch.uint8).data_ptr(), b, h, w, c, kh, kw, sh, sw, ph, pw, dh, dw,
-              out.view(torch.uint8).data_ptr(), _lib.stream_of(x), what="im2col_gather")
-    return out
-
-
-def _fused_pointwise_shape(value: Tensor, pw_weight: Tensor) -> bool:
-    """The one-kernel block's shapes (``flashim/backends/triton/conv.py:561-599``): 128 channels in, 128 x 128
-    pointwise weight."""
-    return value.shape[1] == 128 and tuple(pw_weight.shape) == (128, 128)
-
-
-def depthwise5x5_relu_pointwise_mxfp8(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
-                                      pw_scale_swizzled: Tensor, pw_scale_u8: Tensor, pw_bias: Tensor) -> Tensor:
-    """The MXFP8 refiner block (``flashim/ops/conv.py:93-113``) -> ``[B, C, H, W]`` view of NHWC BF16. At 128 x 128
-    one kernel (``fim_depthwise5x5_relu_pointwise_mxfp8``: the quantized activations stay on chip), else the
-    composite."""
-    if not _fused_pointwise_shape(value, pw_weight):
-        return pointwise_mxfp8_composite(value, dw_weight, dw_bias, pw_weight, pw_scale_swizzled, pw_scale_u8,
-                                         pw_bias)
-    from flashim_amd.backends.hip import gemm
-
-    batch, channels, height, width = value.shape
-    x = _nhwc_bf16(value)
-    dw_w = dw_weight.to(device=value.device, dtype=torch.bfloat16).contiguous()
-    dw_b = dw_bias.to(device=value.device, dtype=torch.float32).contiguous()
-    e8m0 = pw_scale_u8.to(value.device).contiguous().view(torch.uint8)
-    bias, bias_code = gemm._bias(pw_bias, value.device)
-    out = torch.empty(batch, height, width, 128, device=value.device, dtype=torch.bfloat16)
-    _lib.call("fim_depthwise5x5_relu_pointwise_mxfp8", x.data_ptr(), batch, height, width, channels, dw_w.data_ptr(),
-              dw_b.data_ptr(), pw_weight.contiguous().view(torch.uint8).data_ptr(), 128, e8m0.data_ptr(),
-              _lib.ptr(bias), bias_code, out.data_ptr(), _lib.stream_of(value),
-              what=f"depthwise5x5_relu_pointwise_mxfp8 {tuple(value.shape)}")
-    return out.permute(0, 3, 1, 2)
-
-
-def pointwise_mxfp8_composite(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
-                              pw_scale_swizzled: Tensor, pw_scale_u8: Tensor, pw_bias: Tensor) -> Tensor:
-    """Two launches: depthwise producer (dynamic MXFP8) then the block-scaled pointwise GEMM with the weight's plain
-    E8M0 bytes."""
-    from flashim_amd.backends.hip import gemm
-
-    batch, channels, height, width = value.shape
-    quantized, scale = depthwise5x5_relu_mxfp8(value, dw_weight, dw_bias)
-    n, k = pw_weight.shape
-    w_exponent = (pw_scale_u8.view(torch.uint8).to(torch.int16) - 127).to(torch.int8).reshape(n, k // 32)
-    m = quantized.shape[0]
-    bias, bias_code = gemm._bias(pw_bias, value.device)
-    out = torch.empty(m, n, device=value.device, dtype=torch.bfloat16)
-    _lib.call("fim_mxfp8_scaled_mm", quantized.data_ptr(), m, k, scale.view(torch.uint8).data_ptr(),
-              pw_weight.contiguous().view(torch.uint8).data_ptr(), n, w_exponent.contiguous().data_ptr(),
-              _lib.ptr(bias), bias_code, out.data_ptr(), _lib.stream_of(value), what="pointwise mxfp8")
-    return out.reshape(batch, height, width, n).permute(0, 3, 1, 2)
-
-
-def depthwise5x5_relu_pointwise_int8(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
-                                     pw_wscale: Tensor, pw_bias: Tensor, scale: Tensor) -> Tensor:
-    """The INT8 refiner block (``flashim/ops/conv.py:119-138``) -> ``[B, C, H, W]`` view of NHWC BF16: the two-launch
-    composite at every shape. Its INT8 intermediate is 1 byte per element, and on MI355X at 2 x 128 x 400 x 400 the
-    composite measures 84 us against 90 us for the one-kernel ``pointwise_int8_fused``, which gives the same bits."""
-    return pointwise_int8_composite(value, dw_weight, dw_bias, pw_weight, pw_wscale, pw_bias, scale)
-
-
-def pointwise_int8_fused(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor, pw_wscale: Tensor,
-                         pw_bias: Tensor, scale: Tensor) -> Tensor:
-    """One kernel (``fim_depthwise5x5_relu_pointwise_int8``) at C = 128 with a 128 x 128 pointwise weight; bit for bit
-    the composite."""
-    if not _fused_pointwise_shape(value, pw_weight):
-        raise ValueError(f"pointwise_int8_fused needs C = 128 and a 128 x 128 weight, got {tuple(value.shape)}, "
-                         f"{tuple(pw_weight.shape)}")
-    from flashim_amd.backends.hip import gemm
-
-    batch, channels, height, width = value.shape
-    x = _nhwc_bf16(value)
-    dw_w = dw_weight.to(device=value.device, dtype=torch.bfloat16).contiguous()
-    dw_b = dw_bias.to(device=value.device, dtype=torch.float32).contiguous()
-    wscale = pw_wscale.to(device=value.device, dtype=torch.float32).reshape(-1).contiguous()
-    a_scale = scale.to(device=value.device, dtype=torch.float32).reshape(1).contiguous()
-    bias, bias_code = gemm._bias(pw_bias, value.device)
-    out = torch.empty(batch, height, width, 128, device=value.device, dtype=torch.bfloat16)
-    _lib.call("fim_depthwise5x5_relu_pointwise_int8", x.data_ptr(), batch, height, width, channels, dw_w.data_ptr(),
-              dw_b.data_ptr(), pw_weight.contiguous().data_ptr(), 128, wscale.data_ptr(), a_scale.data_ptr(),
-              _lib.ptr(bias), bias_code, out.data_ptr(), _lib.stream_of(value),
-              what=f"depthwise5x5_relu_pointwise_int8 {tuple(value.shape)}")
-    return out.permute(0, 3, 1, 2)
-
-
-def pointwise_int8_composite(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
-                             pw_wscale: Tensor, pw_bias: Tensor, scale: Tensor) -> Tensor:
-    """Two launches: static INT8 producer then ``int8_linear``."""
-    from flashim_amd.backends.hip import gemm
-
-    batch, channels, height, width = value.shape
-    quantized = depthwise5x5_relu_int8(value, dw_weight, dw_bias, scale)
-    out = gemm.int8_linear(quantized, pw_weight, scale, pw_wscale, pw_bias)
-    return out.reshape(batch, height, width, -1).permute(0, 3, 1, 2)
-
-
 def eligible_im2col(x, kh, kw, sh, sw, ph, pw, dh, dw) -> bool:
     return isinstance(x, Tensor) and is_gfx950(x.device) and x.ndim == 4 and x.element_size() == 1
 
@@ -381,17 +309,9 @@ def small_cin_prepare(weight: Tensor, bias: Tensor) -> tuple[Tensor, Tensor]:
 def conv2d_small_cin_quantize_int8(x: Tensor, scale: Tensor, packed: Tensor, bias: Tensor) -> quant.Int8Tensor:
     """``quantize_int8(relu(bf16(conv3x3(x)) + bias))`` -> INT8 NHWC ``[B, H, W, Cout]`` (an :class:`Int8Tensor` with
     ``scale``); ``packed`` from :func:`small_cin_prepare`."""
-    b, cin, h, w = x.shape
-    cout = packed.shape[0]
-    x = x.contiguous()
-    packed = packed.to(x.device).contiguous()
-    bias_t, code = _bias_args(bias, x.device)
-    scale_t = scale.to(device=x.device, dtype=torch.float32).reshape(1).contiguous()
-    out = torch.empty(b, h, w, cout, device=x.device, dtype=torch.int8)
-    _lib.call("fim_conv3x3_small_cin_quantize_int8", x.data_ptr(), b, cin, h, w, packed.data_ptr(), cout,
-              bias_t.data_ptr(), code, scale_t.data_ptr(), out.data_ptr(), _lib.stream_of(x),
-              what=f"conv2d_small_cin_quantize_int8 {tuple(x.shape)} -> {cout}")
-    return quant.Int8Tensor(out, scale)
+    out = library.conv3x3_small_cin_quantize_int8(x.contiguous(), packed.to(x.device).contiguous(),
+                                                  _bias(bias, x.device), _scalar(scale, x.device))
+    return quant.Int8Tensor(out, _same_scale(scale, x.device))
 
 
 def eligible_small_cin(x: Tensor, scale: Tensor, weight: Tensor, bias: Tensor) -> bool:
@@ -412,14 +332,8 @@ def accepts_small_cin(weight: Tensor, bias: Tensor) -> bool:
 
 def bias_relu_quantize_int8(raw: Tensor, bias: Tensor, scale: Tensor) -> quant.Int8Tensor:
     """``quantize_int8(relu(raw + bias))`` of a BF16 NCHW conv output -> INT8 NHWC ``[B, H, W, C]``."""
-    b, c, h, w = raw.shape
-    raw = raw.contiguous()
-    bias_t, code = _bias_args(bias, raw.device)
-    scale_t = scale.to(device=raw.device, dtype=torch.float32).reshape(1).contiguous()
-    out = torch.empty(b, h, w, c, device=raw.device, dtype=torch.int8)
-    _lib.call("fim_bias_relu_quantize_int8", raw.data_ptr(), b, c, h, w, bias_t.data_ptr(), code, scale_t.data_ptr(),
-              out.data_ptr(), _lib.stream_of(raw), what=f"bias_relu_quantize_int8 {tuple(raw.shape)}")
-    return quant.Int8Tensor(out, scale)
+    out = library.bias_relu_quantize_int8(raw.contiguous(), _bias(bias, raw.device), _scalar(scale, raw.device))
+    return quant.Int8Tensor(out, _same_scale(scale, raw.device))
 
 
 def eligible_bias_relu_quantize(raw: Tensor, bias: Tensor, scale: Tensor) -> bool:

@@ -1,5 +1,10 @@
-"""HIP impls of the activation quantize ops (``flashim/ops/quantize.py:80-100``), with the torch references' signatures
-and return types."""
+"""HIP impls of the activation quantize ops (``flashim/ops/quantize.py:63-131``), with the torch references'
+signatures and return types:
+
+* ``quantize_mxfp8`` (``:80-85``) and ``quantize_int8`` (``:91-100``): the static quantizers;
+* ``gelu_quantize`` (``:63-74``) and ``gelu_quantize_int8`` (``:128-131``): GELU (erf form, ``approximate="none"``;
+  the tanh form stays with FlashIM's reference) in the input's dtype, then the same quantizers, in one pass.
+"""
 
 from __future__ import annotations
 
@@ -8,6 +13,8 @@ from torch import Tensor
 
 from flashim_amd import quant
 from flashim_amd.platforms import is_gfx950
+
+_FLOATS = (torch.float32, torch.bfloat16, torch.float16)
 
 
 def quantize_mxfp8(value: Tensor, scale_exponent: Tensor) -> quant.QuantizedTensor:
@@ -22,16 +29,35 @@ def quantize_int8(value: Tensor, scale: Tensor, *, channel_scale: Tensor | None 
     return quant.Int8Tensor(quant.quantize_int8_values(value, scale, channel_scale), scale)
 
 
+def gelu_quantize(value: Tensor, scale_exponent: Tensor, approximate: str = "none", *,
+                  input_bias: Tensor | None = None) -> quant.QuantizedTensor:
+    """``ops.gelu_quantize``: ``quantize_static(GELU(value [+ input_bias]))``."""
+    return quant.gelu_quantize_static(value, scale_exponent, input_bias)
+
+
+def gelu_quantize_int8(value: Tensor, scale: Tensor, approximate: str = "none") -> quant.Int8Tensor:
+    """``ops.gelu_quantize_int8``: ``quantize_int8(GELU(value))``."""
+    return quant.gelu_quantize_int8_static(value, scale)
+
+
 def eligible_quantize_mxfp8(value: Tensor, scale_exponent: Tensor) -> bool:
-    return (
-        isinstance(value, Tensor) and is_gfx950(value.device) and value.ndim >= 2
-        and value.dtype in (torch.float32, torch.bfloat16, torch.float16)
-    )
+    return isinstance(value, Tensor) and is_gfx950(value.device) and value.ndim >= 2 and value.dtype in _FLOATS
 
 
 def eligible_quantize_int8(value: Tensor, scale: Tensor, *, channel_scale: Tensor | None = None) -> bool:
     return (
-        isinstance(value, Tensor) and is_gfx950(value.device) and value.ndim >= 1
-        and value.dtype in (torch.float32, torch.bfloat16, torch.float16) and scale.numel() == 1
-        and (channel_scale is None or channel_scale.numel() == value.shape[-1])
+        isinstance(value, Tensor) and is_gfx950(value.device) and value.ndim >= 1 and value.dtype in _FLOATS
+        and scale.numel() == 1 and (channel_scale is None or channel_scale.numel() == value.shape[-1])
     )
+
+
+def eligible_gelu_quantize(value: Tensor, scale_exponent: Tensor, approximate: str = "none", *,
+                           input_bias: Tensor | None = None) -> bool:
+    return (
+        approximate == "none" and eligible_quantize_mxfp8(value, scale_exponent)
+        and (input_bias is None or input_bias.numel() == value.shape[-1])
+    )
+
+
+def eligible_gelu_quantize_int8(value: Tensor, scale: Tensor, approximate: str = "none") -> bool:
+    return approximate == "none" and eligible_quantize_int8(value, scale)

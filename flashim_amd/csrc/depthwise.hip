@@ -310,6 +310,8 @@ int fim_depthwise5x5(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t
   if (((uintptr_t)x % 8) != 0 || ((uintptr_t)weight % 8) != 0 || ((uintptr_t)out % 8) != 0) return FIM_ERR_UNSUPPORTED;
   if (B * H * W == 0) return FIM_OK;
   if (H > 2147483647LL || W > 2147483647LL) return FIM_ERR_UNSUPPORTED;
+  // 32-bit channel and weight indices ((ky * 5 + kx) * C + c) and 40-bit element offsets
+  if (C > 2147483647LL / 25 || B * H * W > (1LL << 40) / C) return FIM_ERR_UNSUPPORTED;
   if (((uintptr_t)x % 16) != 0) return FIM_ERR_UNSUPPORTED;
   const int64_t tx = cdiv(W, DW_TW), ty = cdiv(H, DW_TH);
   const int64_t ntiles = tx * ty * B * (C / DW_CS);

@@ -50,7 +50,8 @@ struct ConvArgs {
   int64_t res_channels, rs_b, rs_h, rs_w, rs_c;
   const float* out_scale;  // OUT_INT8
   const int8_t* out_expo;  // OUT_E4M3: [Cout / 32]
-  void* out;               // [B, Ho, Wo, Cout]
+  void* out;               // [B, Ho, Wo, Cout]: pixel rows out_ld elements apart (out_ld >= Cout)
+  int64_t out_ld;
   int8_t* pool_out;        // POOL: [B, Ho/2, Wo/2, Cout] int8, the 2x2 max pool of out quantized with out_scale
   int out_mode, relu_pre, relu_post, gelu;  // ReLU before the BF16 rounding / after the residual add
   int B, H, W, Cin, Ho, Wo, Cout;
@@ -62,16 +63,6 @@ struct ConvArgs {
   int m_base;              // first GEMM row of this launch (a split launch runs its last rows as a second launch)
 };
 
-#ifdef FIM_TIMING
-__device__ unsigned long long fim_timing[16384][4];
-#define FIM_STAMP(k) \
-  do { if (threadIdx.x == 0 && blockIdx.x < 16384) fim_timing[blockIdx.x][k] = (wall_clock64() & 0xffffffffffffULL) | ((unsigned long long)__smid() << 48); } while (0)
-extern "C" int fim_debug_timing(void* dst) {
-  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(fim_timing), sizeof(fim_timing), 0, hipMemcpyDeviceToHost);
-}
-#else
-#define FIM_STAMP(k) do { } while (0)
-#endif
 
 constexpr int BM_MAIN = 128;  // pixel rows per tile (the tail of a launch may use 64-row tiles)
 constexpr int KC = 128;          // bytes of K per step
@@ -154,7 +145,7 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
   const bool row_scales = KIND == KIND_INT8 && a.a_scale_rows != nullptr;
   // descriptor operands through readfirstlane: provably uniform, so the descriptor stays in SGPRs (a descriptor the
   // compiler cannot prove uniform turns every store into a readfirstlane loop)
-  const int nbytes = __builtin_amdgcn_readfirstlane((int)((uint32_t)a.M * (uint32_t)a.Cout * ESZ));
+  const int nbytes = __builtin_amdgcn_readfirstlane((int)((uint32_t)a.M * (uint32_t)a.out_ld * ESZ));
   const uint64_t out_addr = (uint64_t)a.out;
   const uint64_t out_u = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(out_addr >> 32)) << 32) |
                          (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)out_addr);
@@ -216,11 +207,7 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
       }
       round_bf16x2(v[0], v[1]);
       round_bf16x2(v[2], v[3]);
-#ifdef FIM_EPI_NOGELU
-      if (false) {
-#else
       if (GELU) {
-#endif
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
         if (RES || OUT == OUT_INT8) {  // a BF16 store's pack and the E4M3 conversion round the same way
@@ -244,12 +231,8 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
       const float* v = y[i];
       const int nbase = n_tile0 + nl0 + i * 16 + 4 * g;
       const bool nvalid = n_tile0 + nl0 + i * 16 < a.Cout;  // whole 16-channel block in or out (Cout % 16 == 0)
-#ifdef FIM_EPI_NOSTORE
-      if (v[0] + v[1] + v[2] + v[3] == 12345.0f) static_cast<uint16_t*>(a.out)[m] = 1;
-      continue;
-#endif
       // rows past M land past the buffer's end; invalid channel blocks are sent there too
-      const uint32_t off = nvalid ? ((uint32_t)m * (uint32_t)a.Cout + (uint32_t)nbase) * ESZ : 0x80000000u;
+      const uint32_t off = nvalid ? ((uint32_t)m * (uint32_t)a.out_ld + (uint32_t)nbase) * ESZ : 0x80000000u;
       if (OUT == OUT_BF16) {
         const uint32_t lo = pack_bf16x2(v[0], v[1]), hi = pack_bf16x2(v[2], v[3]);
         __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rsrc, (int)off, 0, 0);
@@ -281,7 +264,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc
                          a.rs_b == (int64_t)a.Ho * a.Wo * a.Cout && ((uintptr_t)a.residual & 7) == 0 &&
                          (int64_t)a.M * a.Cout * 2 < (int64_t)0x7fffffff;
   if (!POOL && (a.residual == nullptr || res_dense) && (a.Cout & 15) == 0 &&
-      (int64_t)a.M * a.Cout * (OUT == OUT_BF16 ? 2 : 1) < (int64_t)0x7fffffff) {
+      (int64_t)a.M * a.out_ld * (OUT == OUT_BF16 ? 2 : 1) < (int64_t)0x7fffffff) {
     if (a.residual != nullptr) {
       if (a.gelu)
         conv_epilogue_fast<KIND, OUT, MB, NB, true, true>(a, acc_i, acc_f, row0, n_tile0, nl0, ep_scale, ep_bias,
@@ -393,7 +376,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc
           }
         }
       }
-      const int64_t o = (int64_t)px[j] * a.Cout + nbase;
+      const int64_t o = (int64_t)px[j] * a.out_ld + nbase;
       if (POOL) {
         // the window's 4 pixels sit on lanes 4k .. 4k + 3 of this 16-lane group (rows m = 4 * window + 0..3), all
         // valid or all past M together: max across them, quantize (monotonic, so equal to quantizing the max of the
@@ -418,10 +401,6 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc
           }
         }
       }
-#ifdef FIM_EPI_NOSTORE
-      if (y[0] + y[1] + y[2] + y[3] == 12345.0f) static_cast<uint16_t*>(a.out)[o] = 1;
-      continue;
-#endif
       if (OUT == OUT_BF16) {
         uint16_t* dst = static_cast<uint16_t*>(a.out) + o;
         const uint32_t lo = pack_bf16x2(y[0], y[1]), hi = pack_bf16x2(y[2], y[3]);
@@ -479,7 +458,6 @@ __global__ __launch_bounds__(256, ONE ? 3 : 2) void conv_igemm_kernel(const Conv
   // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs (pid % 8), so each XCD takes a
   // contiguous run of tiles; a run walks the N tiles of one M tile back to back, and consecutive M tiles (which share
   // input halo rows) stay on the same XCD's L2.
-  FIM_STAMP(0);
   const int per_xcd = gridDim.x >> 3;
   const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
   if (t >= a.n_tiles * a.m_tiles) return;
@@ -660,7 +638,6 @@ __global__ __launch_bounds__(256, ONE ? 3 : 2) void conv_igemm_kernel(const Conv
   if (!ONE && nk > 1) gload(ra1, rb1, sx1, sw1, bok1);
   sstore(0, ra0, rb0);
   lds_barrier();
-  FIM_STAMP(1);
 
   // one K step from LDS stage `buf`; (rsx, rsw): the raw exponent bytes loaded with it; blk_ok false marks a
   // channel block past Cin (zero data: any scale works, use 2^0)
@@ -724,12 +701,8 @@ __global__ __launch_bounds__(256, ONE ? 3 : 2) void conv_igemm_kernel(const Conv
       for (int j = 0; j < SXN; ++j) sx[j] = sx0[j];
 #pragma unroll
       for (int i = 0; i < NB; ++i) sw[i] = sw0[i];
-#ifndef FIM_EXP_NOLOAD
       if (kt + 2 < nk) gload(ra0, rb0, sx0, sw0, bok0);
-#endif
-#ifndef FIM_EXP_NOMFMA
       compute(0, sx, sw, bok);
-#endif
       __builtin_amdgcn_sched_barrier(0);
       if (kt + 1 < nk) sstore(1, ra1, rb1);
       lds_barrier();
@@ -741,21 +714,15 @@ __global__ __launch_bounds__(256, ONE ? 3 : 2) void conv_igemm_kernel(const Conv
       for (int j = 0; j < SXN; ++j) sx[j] = sx1[j];
 #pragma unroll
       for (int i = 0; i < NB; ++i) sw[i] = sw1[i];
-#ifndef FIM_EXP_NOLOAD
       if (kt + 3 < nk) gload(ra1, rb1, sx1, sw1, bok1);
-#endif
-#ifndef FIM_EXP_NOMFMA
       compute(1, sx, sw, bok);
-#endif
       __builtin_amdgcn_sched_barrier(0);
       if (kt + 2 < nk) sstore(0, ra0, rb0);
       lds_barrier();
     }
   }
 
-  FIM_STAMP(2);
   conv_epilogue<KIND, OUT, POOL, MB, NB>(a, acc_i, acc_f, m0 + wm * (MB * 16), n0, wn * (BN / 2), ep_scale, ep_bias, ep_osc);
-  FIM_STAMP(3);
 }
 
 
@@ -799,13 +766,9 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
   const int wm = wave % WM, wn = wave / WM;
 
   // XCD-aware order as in the 128-row kernel: each XCD takes a contiguous run of tiles, N tiles of an M tile adjacent
-  FIM_STAMP(0);
   const int per_xcd = gridDim.x >> 3;
   const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
   if (t >= a.n_tiles * a.m_tiles) return;
-#ifdef FIM_EXP_EMPTY
-  if (a.M > 0) return;
-#endif
   const int n0 = (t % a.n_tiles) * BN;
   const int m0 = a.m_base + (t / a.n_tiles) * BM;
 
@@ -981,15 +944,8 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
     }
     const bool more = kt + NST - 1 < nk;
     __builtin_amdgcn_sched_barrier(0);
-#ifndef FIM_EXP_NOLOAD
     if (more) issue(nxt, esx[en], esw[en], eok[en]);
-#endif
     __builtin_amdgcn_sched_barrier(0);
-#ifdef FIM_EXP_NOMFMA
-    if (false) {
-#else
-    if (true) {
-#endif
     if constexpr (KIND == KIND_INT8) {
 #pragma unroll
       for (int i = 0; i < NB; ++i)
@@ -1004,10 +960,6 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
 #pragma unroll
         for (int j = 0; j < MB; ++j)
           acc_f[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[i], xf[j], acc_f[i][j], 0, 0, 0, sw[i], 0, sxs);
-    }
-    } else {
-#pragma unroll
-      for (int j = 0; j < MB; ++j) acc_f[0][j][0] += (float)(xf[j][0] ^ xlo[j][0] ^ wf[j % NB][2] ^ wlo[j % NB][3]);
     }
     __builtin_amdgcn_sched_barrier(0);  // the wait for the next stage stays behind this step's MFMAs
     // step kt + 1's loads were issued one step earlier (or in the prologue); when this step issued loads, at least
@@ -1026,7 +978,6 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
     } else {
       vm_lds_barrier();
     }
-    FIM_STAMP(1);
     for (int kt = 0; kt < nk; kt += 3) {
       step(kt, st0, st2, 0, 2);
       if (kt + 1 < nk) step(kt + 1, st1, st0, 1, 0);
@@ -1035,17 +986,14 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
   } else {
     issue(st0, esx[0], esw[0], eok[0]);
     vm_lds_barrier();
-    FIM_STAMP(1);
     for (int kt = 0; kt < nk; kt += 2) {
       step(kt, st0, st1, 0, 1);
       if (kt + 1 < nk) step(kt + 1, st1, st0, 1, 0);
     }
   }
 
-  FIM_STAMP(2);
   conv_epilogue<KIND, OUT, 0, MB, NB>(a, acc_i, acc_f, m0 + wm * (MB * 16), n0, wn * (NB * 16), ep_scale, ep_bias,
                                       ep_osc);
-  FIM_STAMP(3);
 }
 
 template <int KIND, int WM>
@@ -1124,9 +1072,6 @@ static void launch_xs(const ConvArgs& a, int lw, dim3 grid, hipStream_t stream) 
 // per CU; the wavefront grid is the one whose N tiles pad Cout the least (ties: 256-channel tiles).
 // Returns WM (2: 160 x 256 tiles, 4: 320 x 128) or 0.
 static int wide_wm(const ConvArgs& a, int lw) {
-#ifdef FIM_EXP_NO_WIDE
-  return 0;
-#endif
   if (lw != 16 || a.x_swz != nullptr || a.pool_out != nullptr || a.a_scale_rows != nullptr || a.Cout <= 64) return 0;
   if ((int64_t)a.B * a.H * a.W * a.Cin >= (1LL << 31) - 16 || (int64_t)a.Cout * a.kh * a.kw * a.Cin >= (1LL << 31))
     return 0;
@@ -1187,7 +1132,6 @@ static int launch_conv(ConvArgs a, hipStream_t stream) {
   // complete rounds run as one launch and the remaining rows as a second launch of 64 x 64 tiles (4x as many, each
   // about a quarter of the work), which fills the last round instead.
   if (a.x_swz == nullptr && a.pool_out == nullptr) {
-#ifndef FIM_EXP_NO_SMALL
     // fewer 128-row tiles than CUs: 64 x 64 tiles instead, so the launch reaches every CU (e.g. config 1: 128 tiles
     // of 128 x 64 -> 256 of 64 x 64)
     if (tiles < device_cus()) {
@@ -1197,7 +1141,6 @@ static int launch_conv(ConvArgs a, hipStream_t stream) {
       launch_tail<KIND>(t, lw, dim3((unsigned)(cdiv((int64_t)t.m_tiles * t.n_tiles, 8) * 8)), stream);
       return launch_status();
     }
-#endif
     const int64_t slots = 2LL * device_cus();
     const int64_t full = tiles / slots, rem = tiles - full * slots;
     const int64_t mt_main = full * slots / a.n_tiles;
@@ -1246,7 +1189,7 @@ static void fill_epilogue(ConvArgs& a, const void* bias, int bias_dtype, const v
   // with one; linear semantics (ops/gemm.py:91-97, relu_before_residual): always before, the residual added after
   a.relu_pre = relu && (residual == nullptr || relu_before_residual);
   a.relu_post = relu && residual != nullptr && !relu_before_residual;
-  a.gelu = gelu; a.out = out;
+  a.gelu = gelu; a.out = out; a.out_ld = a.Cout;
 }
 
 static bool dims_fit(int64_t B, int64_t H, int64_t W, int64_t Cin, int64_t Cout) {
@@ -1393,6 +1336,31 @@ int fim_int8_linear(const int8_t* a, int64_t M, int64_t K, const int8_t* weight,
   fill_epilogue(c, bias, bias_dtype, residual, res_dtype, res_channels, strides, relu, gelu, out, 1);
   c.out_scale = out_scale;
   c.out_mode = out_scale != nullptr ? OUT_INT8 : OUT_BF16;
+  return launch_conv<KIND_INT8>(c, stream);
+}
+
+// int8_linear's BF16 result statically quantized again for the next INT8 consumer, written into rows out_row_stride
+// bytes apart (e.g. one half of a concatenation buffer): ops/gemm.py:104-116.
+int fim_int8_linear_quantize(const int8_t* a, int64_t M, int64_t K, const int8_t* weight, int64_t N,
+                             const float* a_scale, const float* a_scale_rows, const float* w_scale, const void* bias,
+                             int bias_dtype, const float* out_scale, int8_t* out, int64_t out_row_stride,
+                             hipStream_t stream) {
+  if (a == nullptr || weight == nullptr || (a_scale == nullptr && a_scale_rows == nullptr) || w_scale == nullptr ||
+      out_scale == nullptr || out == nullptr)
+    return FIM_ERR_INVALID;
+  if (out_row_stride < N) return FIM_ERR_INVALID;
+  if (!dims_fit(1, 1, M, K, N) || out_row_stride > 2147483647LL) return FIM_ERR_UNSUPPORTED;
+  ConvArgs c = {};
+  c.x = reinterpret_cast<const uint8_t*>(a);
+  c.w = reinterpret_cast<const uint8_t*>(weight);
+  c.a_scale = a_scale != nullptr ? a_scale : a_scale_rows;
+  c.a_scale_rows = a_scale_rows;
+  c.w_scale = w_scale;
+  fill_geometry(c, 1, 1, M, K, N, 1, 1, 1, 1, 0, 0, 1, 1);
+  fill_epilogue(c, bias, bias_dtype, nullptr, 0, 0, nullptr, 0, 0, out, 1);
+  c.out_ld = out_row_stride;
+  c.out_scale = out_scale;
+  c.out_mode = OUT_INT8;
   return launch_conv<KIND_INT8>(c, stream);
 }
 

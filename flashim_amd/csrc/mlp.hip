@@ -24,12 +24,6 @@ enum { MLP_BLOCK = 0, MLP_REFERENCE = 1 };
 
 constexpr int MLP_C = 64, MLP_H = 256, MLP_BM = 64;
 
-#ifdef FIM_TIMING
-__device__ unsigned long long fim_mlp_timing[1024][4];
-#define MLP_T(k) unsigned long long _t##k = wall_clock64()
-#else
-#define MLP_T(k) do { } while (0)
-#endif
 
 struct MlpArgs {
   const uint8_t* x;        // [P, C] int8 / E4M3
@@ -137,16 +131,10 @@ __global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
   load_res(blockIdx.x, res_cur);
   __syncthreads();  // weights and tables staged
 
-#ifdef FIM_TIMING
-  unsigned long long ph[4] = {0, 0, 0, 0};
-  const unsigned long long t_begin = wall_clock64();
-#endif
   for (int t = blockIdx.x; t < a.ntiles; t += gridDim.x) {
-    MLP_T(0);
     const int px0 = t * MLP_BM;
     *reinterpret_cast<uint4*>(&xs[ld_dst]) = cur;
     __syncthreads();  // input tile staged; the previous tile's hidden reads are done
-    MLP_T(1);
     cur = load_tile(t + gridDim.x);  // prefetch the next tile's input and residual
     load_res(t + gridDim.x, res_nxt);
 
@@ -209,9 +197,7 @@ __global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
             round_bf16x2(y[2], y[3]);
           }
         }
-#ifndef FIM_EXP_NOGELU
         gelu_erf_n<16>(reinterpret_cast<float (&)[16]>(yb));  // the block's 16 GELU chains interleaved
-#endif
         uint32_t qw[4];
         if (KIND == MLP_MX) {  // BF16 rounding and static E4M3 in one step (the lane's 4 channels share a scale block)
           const float sc = hsc[h0], bound = 448.0f * sc;
@@ -238,9 +224,7 @@ __global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
         }
       }
     }
-    MLP_T(2);
     __syncthreads();  // hidden tile complete
-    MLP_T(3);
 
     // ---- contract: wave w computes pixels [16 w, 16 w + 16) x all 64 channels ---------------------------------
     {
@@ -305,23 +289,8 @@ __global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) res_cur[i] = res_nxt[i];
-#ifdef FIM_TIMING
-    const unsigned long long _t4 = wall_clock64();
-    ph[0] += _t1 - _t0; ph[1] += _t2 - _t1; ph[2] += _t3 - _t2; ph[3] += _t4 - _t3;
-#endif
   }
-#ifdef FIM_TIMING
-  if (tid == 0 && blockIdx.x < 1024) {
-    for (int k = 0; k < 4; ++k) fim_mlp_timing[blockIdx.x][k] = ph[k];
-  }
-  (void)t_begin;
-#endif
 }
-#ifdef FIM_TIMING
-extern "C" int fim_debug_mlp_timing(void* dst) {
-  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(fim_mlp_timing), sizeof(fim_mlp_timing), 0, hipMemcpyDeviceToHost);
-}
-#endif
 
 }  // namespace fim
 

@@ -1,6 +1,7 @@
 // Activation / weight quantizers of the quantized conv path (all HBM-bound byte work):
 //   fim_quantize_int8          static per-tensor INT8      flashim/ops/quantize.py:91-100, quant/tensor.py:148-151
 //   fim_quantize_mxfp8         static block-32 MXFP8       flashim/ops/quantize.py:80-85, quant/tensor.py:97-121
+//   fim_gelu_quantize_mxfp8 / _int8   GELU in the input dtype, then either   flashim/ops/quantize.py:63-74, 128-131
 //   fim_quantize_mxfp8_dynamic per-(row, 32) MXFP8 (+ the 128x4 swizzled E8M0 scales)  quant/formats/mx.py:50-86
 //   fim_quantize_int8_rows     per-row INT8 weights / tokens   quant/formats/int8.py:19-27, ops/quantize.py:148-157
 //   fim_calibrate_block32      static exponents from an amax over rows  quant/formats/mx.py:41-47
@@ -23,6 +24,8 @@ struct Geometry4 {
 // ----- output element functions --------------------------------------------------------------------------------
 
 // MODE_INT8: round(x * cs[c] / scale) (IEEE division); MODE_MX: clamp(x / 2^e[c/32], +-448) -> E4M3 (zero padding).
+// gelu != 0 first applies GELU in the input's dtype (the gelu_quantize producers, flashim/ops/quantize.py:63-74,
+// 128-131): x (+ in_bias[c] in FP32) -> erf GELU in FP32 -> rounded to the dtype code `rnd` (FP32: unrounded).
 enum { MODE_INT8 = 0, MODE_MX = 1 };
 
 template <int MODE>
@@ -31,8 +34,17 @@ struct Quantizer {
   float inv;              // INT8 1 / scale
   const float* cs;        // INT8 optional per-channel pre-multiplier (SmoothQuant's 1/s)
   const int8_t* expo;     // MX static exponents [Cpad / 32]
+  int gelu;               // GELU first (uniform)
+  int rnd;                // dtype code the GELU result is rounded to
+  const float* in_bias;   // GELU's optional FP32 input bias [C]
 
   __device__ __forceinline__ uint8_t operator()(float v, int64_t c) const {
+    if (gelu) {
+      if (in_bias != nullptr) v = __fadd_rn(v, in_bias[c]);
+      v = gelu_erf(v);
+      if (rnd == FIM_BF16) v = round_bf16(v);
+      else if (rnd == FIM_F16) v = (float)(_Float16)v;
+    }
     if (MODE == MODE_INT8) {
       if (cs != nullptr) v = v * cs[c];
       return (uint8_t)quantize_int8_fast(v, scale, inv);
@@ -242,7 +254,7 @@ static int launch_quantize(const void* x, Geometry4 g, Quantizer<MODE> qz, const
   const int esize = DT == FIM_F32 ? 4 : 2;
   const bool aligned = ((uintptr_t)x % 16) == 0 && ((uintptr_t)out % 8) == 0;
   const bool packed_all = g.sc == 1 && g.sw == g.C && g.sh == g.W * g.C && g.sb == g.H * g.W * g.C;
-  if (packed_all && Cout == g.C && g.C % 16 == 0 && ((uintptr_t)out % 16) == 0 && aligned &&
+  if (!qz.gelu && packed_all && Cout == g.C && g.C % 16 == 0 && ((uintptr_t)out % 16) == 0 && aligned &&
       rows * g.C < (1LL << 31)) {
     const uint32_t n16 = (uint32_t)(rows * g.C / 16);
     quantize_packed_vec16<DT, MODE><<<dim3((unsigned)cdiv(n16, 256)), dim3(256), 0, stream>>>(
@@ -404,7 +416,7 @@ int fim_quantize_int8(const void* x, int dtype, int64_t B, int64_t H, int64_t W,
                       hipStream_t stream) {
   if (x == nullptr || scale == nullptr || out == nullptr || B < 0 || H < 0 || W < 0 || C < 0) return FIM_ERR_INVALID;
   Geometry4 g{B, H, W, C, sb, sh, sw, sc};
-  Quantizer<MODE_INT8> qz{0.0f, 1.0f, channel_scale, nullptr};
+  Quantizer<MODE_INT8> qz{0.0f, 1.0f, channel_scale, nullptr, 0, 0, nullptr};
   return dispatch_quantize<MODE_INT8>(x, dtype, g, qz, scale, reinterpret_cast<uint8_t*>(out), C, stream);
 }
 
@@ -414,8 +426,26 @@ int fim_quantize_mxfp8(const void* x, int dtype, int64_t B, int64_t H, int64_t W
   if (x == nullptr || exponent == nullptr || out == nullptr || B < 0 || H < 0 || W < 0 || C < 0) return FIM_ERR_INVALID;
   if (Cpad % 32 != 0 || Cpad < C || Cpad - C >= 32) return FIM_ERR_INVALID;
   Geometry4 g{B, H, W, C, sb, sh, sw, sc};
-  Quantizer<MODE_MX> qz{0.0f, 1.0f, nullptr, exponent};
+  Quantizer<MODE_MX> qz{0.0f, 1.0f, nullptr, exponent, 0, 0, nullptr};
   return dispatch_quantize<MODE_MX>(x, dtype, g, qz, nullptr, out, Cpad, stream);
+}
+
+int fim_gelu_quantize_mxfp8(const void* x, int dtype, int64_t B, int64_t H, int64_t W, int64_t C, int64_t sb,
+                            int64_t sh, int64_t sw, int64_t sc, const float* input_bias, const int8_t* exponent,
+                            uint8_t* out, int64_t Cpad, hipStream_t stream) {
+  if (x == nullptr || exponent == nullptr || out == nullptr || B < 0 || H < 0 || W < 0 || C < 0) return FIM_ERR_INVALID;
+  if (Cpad % 32 != 0 || Cpad < C || Cpad - C >= 32) return FIM_ERR_INVALID;
+  Geometry4 g{B, H, W, C, sb, sh, sw, sc};
+  Quantizer<MODE_MX> qz{0.0f, 1.0f, nullptr, exponent, 1, dtype, input_bias};
+  return dispatch_quantize<MODE_MX>(x, dtype, g, qz, nullptr, out, Cpad, stream);
+}
+
+int fim_gelu_quantize_int8(const void* x, int dtype, int64_t B, int64_t H, int64_t W, int64_t C, int64_t sb,
+                           int64_t sh, int64_t sw, int64_t sc, const float* scale, int8_t* out, hipStream_t stream) {
+  if (x == nullptr || scale == nullptr || out == nullptr || B < 0 || H < 0 || W < 0 || C < 0) return FIM_ERR_INVALID;
+  Geometry4 g{B, H, W, C, sb, sh, sw, sc};
+  Quantizer<MODE_INT8> qz{0.0f, 1.0f, nullptr, nullptr, 1, dtype, nullptr};
+  return dispatch_quantize<MODE_INT8>(x, dtype, g, qz, scale, reinterpret_cast<uint8_t*>(out), C, stream);
 }
 
 int fim_quantize_mxfp8_dynamic(const void* x, int dtype, int64_t rows, int64_t K, int64_t row_stride, uint8_t* out,

@@ -100,5 +100,10 @@ def platform_for(device: torch.device | str | None = None) -> Platform:
     return platform
 
 
+@torch.compiler.assume_constant_result  # a process constant per device: keeps dispatch traceable under torch.compile
+def _arch_is_gfx950(device_type: str, index: int | None) -> bool:
+    return platform_for(torch.device(device_type, index)).arch in HIP_ARCHS
+
+
 def is_gfx950(device: torch.device) -> bool:
-    return device.type == "cuda" and platform_for(device).arch in HIP_ARCHS
+    return device.type == "cuda" and _arch_is_gfx950(device.type, device.index)

@@ -16,6 +16,8 @@ import importlib
 import logging
 from collections.abc import Callable
 
+import torch
+
 from flashim_amd import _lib
 from flashim_amd.backends.hip import conv as _conv
 from flashim_amd.backends.hip import gemm as _gemm
@@ -29,6 +31,7 @@ PRIORITY = 2  # above FlashIM's NVIDIA-only impls, which never match "rocm" anyw
 REGISTERED: list[str] = []
 
 
+@torch.compiler.assume_constant_result  # a process constant: keeps FlashIM's dispatch traceable under torch.compile
 def _available() -> bool:
     return _lib.available()
 
@@ -49,7 +52,15 @@ def _adapt_quantized(upstream_tensor_module):
         q = _quantize.quantize_int8(value, scale, channel_scale=channel_scale)
         return upstream_tensor_module.Int8Tensor(q.values, q.scale)
 
-    return quantize_mxfp8, quantize_int8
+    def gelu_quantize(value, scale_exponent, approximate="none", *, input_bias=None):
+        q = _quantize.gelu_quantize(value, scale_exponent, approximate, input_bias=input_bias)
+        return upstream_tensor_module.QuantizedTensor(q.values, q.scale_exponent, q.logical_shape)
+
+    def gelu_quantize_int8(value, scale, approximate="none"):
+        q = _quantize.gelu_quantize_int8(value, scale, approximate)
+        return upstream_tensor_module.Int8Tensor(q.values, q.scale)
+
+    return quantize_mxfp8, quantize_int8, gelu_quantize, gelu_quantize_int8
 
 
 def _as_local(activation, weight):
@@ -108,11 +119,13 @@ def _adapt_stem(upstream_tensor_module):
 
 def impls(upstream_tensor_module) -> dict[str, tuple[Callable, Callable]]:
     """``{op name: (impl, when)}`` for the FlashIM ops this backend replaces."""
-    quantize_mxfp8, quantize_int8 = _adapt_quantized(upstream_tensor_module)
+    quantize_mxfp8, quantize_int8, gelu_quantize, gelu_quantize_int8 = _adapt_quantized(upstream_tensor_module)
     _, bias_relu_quantize_int8 = _adapt_stem(upstream_tensor_module)
     return {
         "quantize_mxfp8": (quantize_mxfp8, _quantize.eligible_quantize_mxfp8),
         "quantize_int8": (quantize_int8, _quantize.eligible_quantize_int8),
+        "gelu_quantize": (gelu_quantize, _quantize.eligible_gelu_quantize),
+        "gelu_quantize_int8": (gelu_quantize_int8, _quantize.eligible_gelu_quantize_int8),
         "int8_conv2d": (_conv.int8_conv2d, _conv.eligible_int8_conv2d),
         "mxfp8_conv2d": (_conv.mxfp8_conv2d, _conv.eligible_mxfp8_conv2d),
         "depthwise5x5_relu_mxfp8": (_conv.depthwise5x5_relu_mxfp8, _conv.eligible_depthwise),
@@ -123,6 +136,7 @@ def impls(upstream_tensor_module) -> dict[str, tuple[Callable, Callable]]:
         "im2col_gather": (_conv.im2col_gather, _conv.eligible_im2col),
         "int8_conv2d_maxpool": (_conv.int8_conv2d_maxpool, _conv.eligible_int8_conv2d_maxpool),
         "int8_linear": (_gemm.int8_linear, _gemm.eligible_int8_linear),
+        "int8_linear_quantize": (_gemm.int8_linear_quantize, _gemm.eligible_int8_linear_quantize),
         "mxfp8_scaled_mm": (_gemm.mxfp8_scaled_mm, _gemm.eligible_mxfp8_scaled_mm),
         "mxfp8_linear": (_mxfp8_linear, _eligible_mxfp8_linear),
         "mxfp8_gelu_mlp": (_mxfp8_gelu_mlp, _eligible_mxfp8_gelu_mlp),

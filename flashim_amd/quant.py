@@ -20,7 +20,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor
 
-from flashim_amd import _lib
+from flashim_amd import _lib, library
 
 FP8_MAX = 448.0
 INT8_MAX = 127.0
@@ -41,22 +41,6 @@ def _dtype_code(t: Tensor, what: str) -> int:
     if code is None:
         raise TypeError(f"{what}: unsupported dtype {t.dtype}")
     return code
-
-
-def geometry4(x: Tensor) -> tuple[Tensor, tuple[int, int, int, int], tuple[int, int, int, int]]:
-    """``x [..., C]`` as ``[B, H, W, C]`` sizes and element strides without copying when possible (leading dims that
-    cannot merge are made contiguous)."""
-    if x.ndim == 0:
-        raise ValueError("expected a channelized tensor")
-    if x.ndim > 4:
-        lead = x.shape[:-3]
-        try:
-            x = x.view(-1, *x.shape[-3:])
-        except RuntimeError:
-            x = x.reshape(math.prod(lead), *x.shape[-3:])
-    while x.ndim < 4:
-        x = x.unsqueeze(0)
-    return x, tuple(x.shape), tuple(x.stride())
 
 
 @dataclass(frozen=True)
@@ -148,28 +132,40 @@ def quantize_static(value: Tensor, scale_exponent: Tensor) -> QuantizedTensor:
     if value.ndim < 2:
         raise ValueError(f"Expected a channelized tensor, got {tuple(value.shape)}")
     _require_gpu(value, "quantize_static")
-    channels = value.shape[-1]
-    padded = padded_channels(channels)
+    _dtype_code(value, "quantize_static")
+    padded = padded_channels(value.shape[-1])
     scale_exponent = scale_exponent.to(device=value.device, dtype=torch.int8).contiguous()
     if tuple(scale_exponent.shape) != (padded // BLOCK,):
         raise ValueError(f"Expected scale shape {(padded // BLOCK,)}, got {tuple(scale_exponent.shape)}")
-    x, (b, h, w, c), (sb, sh, sw, sc) = geometry4(value)
-    out = torch.empty((*value.shape[:-1], padded), device=value.device, dtype=torch.float8_e4m3fn)
-    _lib.call("fim_quantize_mxfp8", x.data_ptr(), _dtype_code(value, "quantize_static"), b, h, w, c, sb, sh, sw, sc,
-              scale_exponent.data_ptr(), out.data_ptr(), padded, _lib.stream_of(value), what="quantize_mxfp8")
-    return QuantizedTensor(out, scale_exponent, tuple(value.shape))
+    codes = library.quantize_mxfp8(value, scale_exponent, padded)
+    return QuantizedTensor(codes.view(torch.float8_e4m3fn), scale_exponent, tuple(value.shape))
+
+
+def gelu_quantize_static(value: Tensor, scale_exponent: Tensor, input_bias: Tensor | None = None) -> QuantizedTensor:
+    """``quantize_static(GELU(value [+ input_bias]))``, GELU (erf form) rounded to ``value``'s dtype
+    (``flashim/ops/quantize.py:63-74``)."""
+    if value.ndim < 2:
+        raise ValueError(f"Expected a channelized tensor, got {tuple(value.shape)}")
+    _require_gpu(value, "gelu_quantize")
+    _dtype_code(value, "gelu_quantize")
+    padded = padded_channels(value.shape[-1])
+    scale_exponent = scale_exponent.to(device=value.device, dtype=torch.int8).contiguous()
+    if tuple(scale_exponent.shape) != (padded // BLOCK,):
+        raise ValueError(f"Expected scale shape {(padded // BLOCK,)}, got {tuple(scale_exponent.shape)}")
+    if input_bias is not None:
+        input_bias = input_bias.to(device=value.device, dtype=torch.float32).contiguous()
+    codes = library.gelu_quantize_mxfp8(value, scale_exponent, padded, input_bias)
+    return QuantizedTensor(codes.view(torch.float8_e4m3fn), scale_exponent, tuple(value.shape))
 
 
 def quantize_int8_values(value: Tensor, scale: Tensor, channel_scale: Tensor | None = None) -> Tensor:
     """``round(value * channel_scale / scale)`` saturated to +-127, packed int8 of ``value``'s shape."""
     _require_gpu(value, "quantize_int8")
-    x, (b, h, w, c), (sb, sh, sw, sc) = geometry4(value)
-    out = torch.empty(value.shape, device=value.device, dtype=torch.int8)
+    _dtype_code(value, "quantize_int8")
+    scale = scale.to(device=value.device, dtype=torch.float32).reshape(1)
     if channel_scale is not None:
         channel_scale = channel_scale.to(device=value.device, dtype=torch.float32).contiguous()
-    _lib.call("fim_quantize_int8", x.data_ptr(), _dtype_code(value, "quantize_int8"), b, h, w, c, sb, sh, sw, sc,
-              scale.data_ptr(), _lib.ptr(channel_scale), out.data_ptr(), _lib.stream_of(value), what="quantize_int8")
-    return out
+    return library.quantize_int8(value, scale, channel_scale)
 
 
 def quantize_int8_static(value: Tensor, scale: Tensor) -> Int8Tensor:
@@ -178,50 +174,45 @@ def quantize_int8_static(value: Tensor, scale: Tensor) -> Int8Tensor:
     return Int8Tensor(quantize_int8_values(value, scale), scale)
 
 
+def gelu_quantize_int8_static(value: Tensor, scale: Tensor) -> Int8Tensor:
+    """``quantize_int8_static(GELU(value))``, GELU rounded to ``value``'s dtype (``flashim/ops/quantize.py:128-131``)."""
+    _require_gpu(value, "gelu_quantize_int8")
+    _dtype_code(value, "gelu_quantize_int8")
+    scale = scale.to(device=value.device, dtype=torch.float32).reshape(())
+    return Int8Tensor(library.gelu_quantize_int8(value, scale.reshape(1)), scale)
+
+
+def _dynamic_input(value: Tensor, what: str) -> Tensor:
+    if value.ndim != 2:
+        raise ValueError(f"Expected a matrix, got shape {tuple(value.shape)}")
+    if value.shape[1] % BLOCK:
+        raise ValueError(f"MXFP8 requires K divisible by 32, got K={value.shape[1]}")
+    _require_gpu(value, what)
+    _dtype_code(value, what)
+    if value.stride(1) != 1 or (value.stride(0) * value.element_size()) % 16:
+        value = value.contiguous()
+    return value  # a view at an unaligned offset is copied inside the op (not traceable here)
+
+
 def quantize_dynamic_2d(value: Tensor) -> tuple[Tensor, Tensor]:
     """Per-(row, 32-block) dynamic MXFP8 of ``[rows, K]``: E4M3 values and int8 exponents ``[rows, K/32]``
     (``flashim/quant/formats/mx.py:50-60``)."""
-    if value.ndim != 2:
-        raise ValueError(f"Expected a matrix, got shape {tuple(value.shape)}")
-    rows, cols = value.shape
-    if cols % BLOCK:
-        raise ValueError(f"MXFP8 requires K divisible by 32, got K={cols}")
-    _require_gpu(value, "quantize_dynamic_2d")
-    if value.stride(1) != 1 or (value.stride(0) * value.element_size()) % 16 or value.data_ptr() % 16:
-        value = value.contiguous()
-    out = torch.empty((rows, cols), device=value.device, dtype=torch.float8_e4m3fn)
-    exponent = torch.empty((rows, cols // BLOCK), device=value.device, dtype=torch.int8)
-    _lib.call("fim_quantize_mxfp8_dynamic", value.data_ptr(), _dtype_code(value, "quantize_dynamic_2d"), rows, cols,
-              value.stride(0), out.data_ptr(), exponent.data_ptr(), None, _lib.stream_of(value))
-    return out, exponent
+    codes, exponent = library.quantize_mxfp8_dynamic(_dynamic_input(value, "quantize_dynamic_2d"), False)
+    return codes.view(torch.float8_e4m3fn), exponent
 
 
 def quantize_dynamic_swizzled(value: Tensor) -> tuple[Tensor, Tensor]:
     """:func:`quantize_dynamic_2d` with the scales written straight into the swizzled E8M0 layout."""
-    rows, cols = value.shape
-    if cols % BLOCK:
-        raise ValueError(f"MXFP8 requires K divisible by 32, got K={cols}")
-    _require_gpu(value, "quantize_dynamic_swizzled")
-    if value.stride(1) != 1 or (value.stride(0) * value.element_size()) % 16 or value.data_ptr() % 16:
-        value = value.contiguous()
-    out = torch.empty((rows, cols), device=value.device, dtype=torch.float8_e4m3fn)
-    swizzled = swizzled_buffer(rows, cols // BLOCK, value.device)
-    _lib.call("fim_quantize_mxfp8_dynamic", value.data_ptr(), _dtype_code(value, "quantize_dynamic_swizzled"), rows,
-              cols, value.stride(0), out.data_ptr(), None, swizzled.data_ptr(), _lib.stream_of(value))
-    return out, swizzled.view(torch.float8_e8m0fnu)
+    codes, swizzled = library.quantize_mxfp8_dynamic(_dynamic_input(value, "quantize_dynamic_swizzled"), True)
+    return codes.view(torch.float8_e4m3fn), swizzled.view(torch.float8_e8m0fnu)
 
 
 def weight_scales_and_values(weight: Tensor) -> tuple[Tensor, Tensor]:
     """Per-output-channel symmetric INT8 of an ``[N, K]`` weight: ``(q, scale)`` with ``scale = safe_scale(amax/127)``
     (``flashim/quant/formats/int8.py:19-27``, as ``StaticInt8Conv2d.from_conv`` uses them)."""
     _require_gpu(weight, "weight_scales")
-    weight = weight.contiguous()
-    rows, k = weight.shape
-    q = torch.empty((rows, k), device=weight.device, dtype=torch.int8)
-    scale = torch.empty(rows, device=weight.device, dtype=torch.float32)
-    _lib.call("fim_quantize_int8_rows", weight.data_ptr(), _dtype_code(weight, "weight_scales"), rows, k, k, 0,
-              q.data_ptr(), scale.data_ptr(), _lib.stream_of(weight))
-    return q, scale
+    _dtype_code(weight, "weight_scales")
+    return library.quantize_int8_rows(weight.contiguous(), False)
 
 
 def calibrate_block32_exponent(value: Tensor) -> Tensor:
@@ -229,17 +220,11 @@ def calibrate_block32_exponent(value: Tensor) -> Tensor:
     if value.ndim < 2:
         raise ValueError(f"Expected a channelized tensor, got {tuple(value.shape)}")
     _require_gpu(value, "calibrate_block32_exponent")
+    _dtype_code(value, "calibrate_block32_exponent")
     matrix = value.reshape(-1, value.shape[-1])
     if matrix.stride(1) != 1:
         matrix = matrix.contiguous()
-    channels = matrix.shape[1]
-    groups = padded_channels(channels) // BLOCK
-    workspace = torch.empty(groups, device=value.device, dtype=torch.int32)
-    exponent = torch.empty(groups, device=value.device, dtype=torch.int8)
-    _lib.call("fim_calibrate_block32", matrix.data_ptr(), _dtype_code(matrix, "calibrate_block32_exponent"),
-              matrix.shape[0], channels, matrix.stride(0), workspace.data_ptr(), exponent.data_ptr(),
-              _lib.stream_of(value))
-    return exponent
+    return library.calibrate_block32(matrix)
 
 
 # -- E8M0 layouts (byte permutations) ------------------------------------------------------------------------------
@@ -251,14 +236,6 @@ def exponent_to_e8m0(exponent: Tensor) -> Tensor:
 
 def swizzled_size(rows: int, groups: int) -> int:
     return ((rows + 127) // 128) * 128 * ((groups + 3) // 4) * 4
-
-
-def swizzled_buffer(rows: int, groups: int, device: torch.device) -> Tensor:
-    """A swizzled-scale buffer; zero-filled where the layout pads rows or groups, as ``swizzle_scales`` pads."""
-    size = swizzled_size(rows, groups)
-    if rows % 128 or groups % 4:
-        return torch.zeros(size, device=device, dtype=torch.uint8)
-    return torch.empty(size, device=device, dtype=torch.uint8)
 
 
 def swizzle_scales(exponent: Tensor) -> Tensor:

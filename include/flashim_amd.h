@@ -45,6 +45,18 @@ int fim_quantize_mxfp8(const void* x, int dtype, int64_t B, int64_t H, int64_t W
                        int64_t sw, int64_t sc, const int8_t* exponent, uint8_t* out, int64_t Cpad,
                        hipStream_t stream);
 
+/* GELU (erf form) then static block-32 MXFP8, fim_quantize_mxfp8's geometry and output: v = x (+ input_bias[c] in
+ * FP32, input_bias may be NULL), g = gelu(v) in FP32 rounded to x's dtype, out = e4m3(clamp(g / 2^exponent[c/32],
+ * +-448)). Replaces ops.gelu_quantize with approximate="none" (flashim/ops/quantize.py:63-74). */
+int fim_gelu_quantize_mxfp8(const void* x, int dtype, int64_t B, int64_t H, int64_t W, int64_t C, int64_t sb,
+                            int64_t sh, int64_t sw, int64_t sc, const float* input_bias, const int8_t* exponent,
+                            uint8_t* out, int64_t Cpad, hipStream_t stream);
+
+/* GELU (erf form) in x's dtype then static per-tensor INT8 with *scale, fim_quantize_int8's geometry and output.
+ * Replaces ops.gelu_quantize_int8 with approximate="none" (flashim/ops/quantize.py:128-131). */
+int fim_gelu_quantize_int8(const void* x, int dtype, int64_t B, int64_t H, int64_t W, int64_t C, int64_t sb,
+                           int64_t sh, int64_t sw, int64_t sc, const float* scale, int8_t* out, hipStream_t stream);
+
 /* Dynamic per-(row, 32) MXFP8 of a [rows, K] matrix (K % 32 == 0, row stride in elements, 16-byte aligned rows):
  * E4M3 out [rows, K] (packed), exponent [rows, K/32] int8 (may be NULL), and the E8M0 scales in cuBLAS' 128x4
  * swizzled layout (may be NULL; its padding bytes are not written, the caller zero-fills them).
@@ -103,11 +115,19 @@ int fim_int8_conv2d_maxpool(const int8_t* x, int64_t B, int64_t H, int64_t W, in
 /* INT8 GEMM a [M, K] x weight [N, K]^T with int8_linear's epilogue: acc * (a_scale * w_scale[n]) + bias[n] (two
  * roundings), ReLU, BF16, GELU if gelu, then + residual [M, res_channels] (row stride res_row_stride) in FP32 -> BF16.
  * a_scale_rows [M] (per-row dynamic activation scales) replaces *a_scale when non-NULL. out BF16 [M, N], or INT8 with
- * out_scale. Replaces ops.int8_linear (flashim/ops/gemm.py:78-101) and int8_linear_quantize (:104-116). */
+ * out_scale. Replaces ops.int8_linear (flashim/ops/gemm.py:78-101). */
 int fim_int8_linear(const int8_t* a, int64_t M, int64_t K, const int8_t* weight, int64_t N, const float* a_scale,
                     const float* a_scale_rows, const float* w_scale, const void* bias, int bias_dtype, int relu, int gelu,
                     const void* residual, int res_dtype, int64_t res_channels, int64_t res_row_stride,
                     const float* out_scale, void* out, hipStream_t stream);
+
+/* int8_linear (no ReLU, GELU or residual) statically quantized again to INT8 with *out_scale, written into out rows
+ * out_row_stride bytes apart (out_row_stride >= N: e.g. one half of a concatenation buffer).
+ * Replaces ops.int8_linear_quantize (flashim/ops/gemm.py:104-116). */
+int fim_int8_linear_quantize(const int8_t* a, int64_t M, int64_t K, const int8_t* weight, int64_t N,
+                             const float* a_scale, const float* a_scale_rows, const float* w_scale, const void* bias,
+                             int bias_dtype, const float* out_scale, int8_t* out, int64_t out_row_stride,
+                             hipStream_t stream);
 
 /* Block-scaled MXFP8 GEMM: a [M, K] E4M3 with per-(row, 32) E8M0 scales in cuBLAS' 128x4 swizzled layout, weight
  * [N, K] E4M3 with int8 exponents [N, K/32] -> BF16 [M, N] (+ bias). Replaces ops.mxfp8_scaled_mm

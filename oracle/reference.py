@@ -167,9 +167,18 @@ def quantize_int8(value: Tensor, scale: Tensor, channel_scale: Tensor | None = N
     return quantize_int8_static(value, scale)
 
 
-def gelu_quantize(value: Tensor, scale_exponent: Tensor, approximate: str = "none") -> Tensor:
-    """ops/quantize.py:63-71 (no input bias)."""
+def gelu_quantize(value: Tensor, scale_exponent: Tensor, approximate: str = "none", *,
+                  input_bias: Tensor | None = None) -> Tensor:
+    """ops/quantize.py:63-74: GELU in value's dtype, or in FP32 of value + input_bias rounded back to value's dtype."""
+    if input_bias is not None:
+        activated = F.gelu(value.float() + input_bias.float(), approximate=approximate).to(value.dtype)
+        return quantize_static(activated, scale_exponent)
     return quantize_static(F.gelu(value, approximate=approximate), scale_exponent)
+
+
+def gelu_quantize_int8(value: Tensor, scale: Tensor, approximate: str = "none") -> Tensor:
+    """ops/quantize.py:128-131."""
+    return quantize_int8_static(F.gelu(value, approximate=approximate), scale)
 
 
 # -- ops/gemm.py -------------------------------------------------------------------------------------------------
@@ -190,6 +199,12 @@ def int8_linear(a: Tensor, weight: Tensor, a_scale: Tensor, w_scale: Tensor, bia
     if residual is not None:
         out = residual + out
     return out
+
+
+def int8_linear_quantize(a: Tensor, weight: Tensor, a_scale: Tensor, w_scale: Tensor, bias: Tensor | None,
+                         out_scale: Tensor) -> Tensor:
+    """ops/gemm.py:104-116: the INT8 values the reference copies into ``out``."""
+    return quantize_int8_static(int8_linear(a, weight, a_scale, w_scale, bias), out_scale)
 
 
 def int8_accumulators(a: Tensor, weight: Tensor) -> Tensor:

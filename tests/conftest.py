@@ -25,10 +25,8 @@ def pytest_collection_modifyitems(config, items):
 
 @pytest.fixture(autouse=True)
 def _reset_ops():
-    from flashim_amd import registry
+    from flashim_amd import dispatch
 
-    registry.configure(os.environ.get("FLASHIM_OPS"))
-    registry.set_strict(False)
+    dispatch.configure(os.environ.get("FLASHIM_OPS"))
     yield
-    registry.configure(None)
-    registry.set_strict(False)
+    dispatch.configure(None)

@@ -1,7 +1,7 @@
 """CPU tests of everything but the GPU compute: the C-ABI library loads and exports every symbol the header declares,
-the host build of the kernels' scalar numerics matches torch exhaustively, the op registry keeps FlashIM's dispatch
-semantics (flashim/ops/_registry.py; its tests tests/unit/test_registry.py), platform detection, the no-fallback
-rule, and the host-side layout / packing helpers."""
+the host build of the kernels' scalar numerics matches torch exhaustively, the dispatcher's selection rules
+(priority, when / accepts, pins and FLASHIM_OPS overrides, bind / prepare, profiler ranges), platform detection, the
+no-fallback rule, and the host-side layout / packing helpers."""
 
 import ctypes
 import re
@@ -12,7 +12,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from flashim_amd import _lib, blocks, ops, quant, registry
+from flashim_amd import _lib, blocks, dispatch, ops, quant
 from flashim_amd.platforms import Feature, Platform, rocm_features
 from oracle import reference as ref
 
@@ -52,6 +52,23 @@ def test_argument_errors_are_reported_without_a_gpu():
         _lib.check(99, "x")
     with pytest.raises(RuntimeError, match="code 7"):
         _lib.check(7, "x")
+
+
+def test_depthwise_rejects_channel_counts_past_its_32_bit_indexing():
+    lib = _lib.load()
+    fake = 1 << 20  # 16-byte aligned stand-ins: the call must return before touching memory or launching
+    c = 85899360  # a multiple of 32 above INT32_MAX / 25 (the weight index (ky * 5 + kx) * C + c)
+    assert lib.fim_depthwise5x5(fake, 1, 1, 1, c, fake, fake, 0, 2, None, None, fake, None, None,
+                                None) == _lib.FIM_ERR_UNSUPPORTED
+    assert lib.fim_depthwise5x5(fake, 1 << 20, 1 << 10, 1 << 10, 32, fake, fake, 0, 2, None, None, fake, None, None,
+                                None) == _lib.FIM_ERR_UNSUPPORTED  # 2^45 elements
+
+
+def test_int8_linear_quantize_rejects_a_row_stride_below_n():
+    lib = _lib.load()
+    fake = 1 << 20
+    assert lib.fim_int8_linear_quantize(fake, 4, 32, fake, 16, fake, None, fake, None, 0, fake, fake, 8,
+                                        None) == _lib.FIM_ERR_INVALID
 
 
 # -- host build of the scalar numerics ---------------------------------------------------------------------------
@@ -108,70 +125,83 @@ def test_host_bf16_and_int8_rounding_match_torch():
     assert np.array_equal(got, ref.quantize_int8_static(y, torch.tensor(0.37)).numpy())
 
 
-# -- the registry (FlashIM semantics) ----------------------------------------------------------------------------
+# -- the dispatcher ----------------------------------------------------------------------------------------------
 
 
 def _toy_op(name):
-    registry.OPS.pop(name, None)
-    op = registry.Op(name, lambda x: ("ref", x))
-    cpu = registry.DeviceSpec("cpu")
+    dispatch.OPS.pop(name, None)
+    op = dispatch.Op(name)
+    cpu = dispatch.DeviceSpec("cpu")
     op.register("low", device=cpu, priority=0)(lambda x: ("low", x))
     op.register("high", device=cpu, priority=1, when=lambda x: x > 0)(lambda x: ("high", x))
     op.register("optin", device=cpu, priority=-1)(lambda x: ("optin", x))
-    op.register("rocm", device=registry.DeviceSpec("rocm"), requires=[Feature.HIP])(lambda x: ("rocm", x))
+    op.register("rocm", device=dispatch.DeviceSpec("rocm"), requires=[Feature.HIP])(lambda x: ("rocm", x))
     return op
 
 
-def test_registry_dispatch_order_when_optin_and_pins():
+def test_dispatch_order_when_optin_and_pins():
     op = _toy_op("toy_dispatch")
     t = torch.tensor(1.0)
     assert op(t)[0] == "high"
-    assert op(-t)[0] == "low"  # when() rejects -> next candidate
+    assert op(-t)[0] == "low"  # when() refuses -> next impl
     assert op.get("optin")(t)[0] == "optin"  # negative priority: only pinned
-    assert op.get("reference")(t)[0] == "ref"
-    assert op.get("high")(-t)[0] == "ref"  # a pinned impl that does not apply runs the reference
+    with pytest.raises(NotImplementedError, match="when"):
+        op.get("high")(-t)  # a pinned impl that does not apply raises: there is no fallback
     report = op.explain(-t)
-    assert report["low"] == "selected" and report["high"] == "when() rejected the arguments"
-    assert report["rocm"].startswith("device") and report["reference"] == "fallback"
-    assert op.supports(t)
+    assert report["low"] == "selected" and report["high"] == "when() refused the arguments"
+    assert report["rocm"].startswith("registered for rocm") and report["optin"].startswith("opt-in")
+    assert op.supports(t) and op.get(None) is op
     with pytest.raises(ValueError):
         op.get("missing")
     with pytest.raises(ValueError):
-        op.register("low", device=registry.DeviceSpec("cpu"))
+        op.register("low", device=dispatch.DeviceSpec("cpu"))
 
 
-def test_registry_overrides_strict_mode_and_counts():
+def test_dispatch_overrides_and_counts():
     op = _toy_op("toy_overrides")
     t = torch.tensor(1.0)
-    registry.configure("toy_overrides:low")
+    dispatch.configure("toy_overrides:low")
     assert op(t)[0] == "low"
-    registry.configure("-toy_overrides")
-    assert op(t)[0] == "ref"
-    registry.configure(None)
+    dispatch.configure("-toy_overrides")
+    with pytest.raises(NotImplementedError, match="switched off"):
+        op(t)
+    assert not op.supports(t)
+    dispatch.configure(None)
     with pytest.raises(ValueError):
-        registry.configure("bogus")
-    registry.reset_call_counts()
+        dispatch.configure("bogus")
+    dispatch.reset_call_counts()
     op(t), op(-t)
-    assert registry.call_counts()["toy_overrides"] == {"high": 1, "low": 1}
+    assert dispatch.call_counts()["toy_overrides"] == {"high": 1, "low": 1}
 
 
-def test_registry_bind_prepares_once():
-    registry.OPS.pop("toy_bind", None)
-    op = registry.Op("toy_bind", lambda x, w: x + w, weights=1)
+def test_dispatch_profiler_range_names_op_and_impl():
+    op = _toy_op("toy_range")
+    with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CPU]) as prof:
+        op(torch.tensor(1.0))
+    assert any(e.name == "flashim::toy_range[high]" for e in prof.events())
+
+
+def test_dispatch_bind_prepares_once():
+    dispatch.OPS.pop("toy_bind", None)
+    op = dispatch.Op("toy_bind", weights=1)
     calls = []
-    op.register("packed", device=registry.DeviceSpec("cpu"),
+    op.register("packed", device=dispatch.DeviceSpec("cpu"),
                 prepare=lambda w: (calls.append(1) or w * 10,))(lambda x, w: x + w)
+    op.register("plain", device=dispatch.DeviceSpec("cpu"), priority=-1)(lambda x, w: x - w)
     bound = op.bind(torch.tensor(1.0)).warmup()
-    assert bound.primary == "packed" and len(calls) == 1
+    assert bound.primary == "packed" and bound.available == ["packed"] and len(calls) == 1
     assert bound(torch.tensor(2.0)).item() == 12.0 and bound(torch.tensor(3.0)).item() == 13.0
     assert len(calls) == 1
+    assert op.bind(torch.tensor(1.0), impl="plain")(torch.tensor(5.0)).item() == 4.0
+    with pytest.raises(ValueError):
+        op.bind()
 
 
 def test_platform_features():
     assert rocm_features("gfx950") >= {Feature.HIP, Feature.MFMA_I8, Feature.MFMA_F8F6F4_SCALED, Feature.FP8_E4M3}
     assert Feature.HIP not in rocm_features("gfx942")  # other AMD architectures never select the gfx950 kernels
     p = Platform("rocm", 0, arch="gfx942", features=rocm_features("gfx942"))
-    assert not registry.DeviceSpec("cuda").matches(p) and registry.DeviceSpec("rocm").matches(p)
+    assert not dispatch.DeviceSpec("cuda").matches(p) and dispatch.DeviceSpec("rocm").matches(p)
 
 
 def test_ops_have_no_cpu_fallback():

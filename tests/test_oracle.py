@@ -22,11 +22,14 @@ def test_exponent_rule_known_answers():
 
 
 def test_exponent_rule_is_smallest_power_fitting_448():
-    amax = torch.rand(10000) * torch.exp2(torch.randint(-60, 60, (10000,)).float()) + 1e-30
+    g = torch.Generator().manual_seed(0)
+    amax = torch.rand(10000, generator=g) * torch.exp2(torch.randint(-60, 60, (10000,), generator=g).float()) + 1e-30
     e = ref.scale_exponent_from_amax(amax).double()
     scaled = amax.double() / torch.exp2(e)
-    assert (scaled <= 448 * (1 + 2**-20)).all()  # fits (up to log2's FP32 rounding at a power of two)
-    assert (amax.double() / torch.exp2(e - 1) > 448 * (1 - 2**-20)).all()  # one smaller power would not
+    # fits, up to FP32 log2's rounding just above a power of two: log2(2^k (1 + d)) rounds to k when d is under about
+    # half an ulp of k (2^-17 relative for |k| < 64)
+    assert (scaled <= 448 * (1 + 2**-17)).all()
+    assert (amax.double() / torch.exp2(e - 1) > 448 * (1 - 2**-17)).all()  # one smaller power would not
 
 
 @pytest.mark.parametrize("channels", [32, 1000, 1024])
@@ -249,6 +252,212 @@ def test_small_cin_oracle_against_float64():
     want = ((F.relu(exact + bias.view(1, -1, 1, 1)).float() / 0.04).round().clamp(-127, 127)).permute(0, 2, 3, 1)
     assert got.shape == (2, 23, 37, 32) and got.dtype == torch.int8
     assert (got.float() - want).abs().max() <= 1 and (got.float() != want).float().mean() < 1e-3
+
+
+# -- pins of the remaining checker functions --------------------------------------------------------------------
+
+
+def _bf16_np(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even of float32 values to BF16 by bit manipulation (independent of torch's conversion)."""
+    bits = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+    rounded = (bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFF0000
+    return rounded.astype(np.uint32).view(np.float32)
+
+
+def _gelu64(x: np.ndarray) -> np.ndarray:
+    """0.5 x (1 + erf(x / sqrt 2)) in float64 (math.erf), the exact-erf GELU."""
+    erf = np.vectorize(math.erf)
+    return 0.5 * x * (1.0 + erf(x / math.sqrt(2.0)))
+
+
+def _mx_operand(rows, k, seed):
+    g = torch.Generator().manual_seed(seed)
+    values = (torch.randn(rows, k, generator=g) * 4).to(torch.float8_e4m3fn)
+    exponent = torch.randint(-9, 4, (rows, k // 32), dtype=torch.int8, generator=g)
+    dense = values.double() * torch.exp2(exponent.double()).repeat_interleave(32, dim=1)
+    return values, exponent, dense
+
+
+def test_mxfp8_scaled_mm_against_float64_of_dequantized_operands():
+    """ops/gemm.py:21-52: a [M, K] with per-(row, 32) swizzled scales times b_t [K, N] (K != N, so a transposed b_t or
+    swapped scale operands cannot pass) + bias, one BF16 rounding."""
+    a, ae, ad = _mx_operand(150, 96, 0)
+    b, be, bd = _mx_operand(40, 96, 1)  # b = b_t^T [N, K]
+    bias = torch.randn(40).to(torch.bfloat16)
+    out = ref.mxfp8_scaled_mm(a, b.t(), ref.swizzle_scales(ae), ref.swizzle_scales(be), bias)
+    exact = ad @ bd.t() + bias.double()
+    mag = ad.abs() @ bd.abs().t() + bias.double().abs()
+    assert out.shape == (150, 40) and out.dtype == torch.bfloat16
+    assert ((out.double() - exact).abs() <= exact.abs() * 2**-8 + mag * 2**-20).all()
+    swapped = ref.mxfp8_scaled_mm(a, b.t(), ref.swizzle_scales(ae), ref.swizzle_scales(torch.roll(be, 1, 0)), bias)
+    assert not torch.equal(swapped, out)
+
+
+def test_mxfp8_gelu_mlp_against_explicit_step_chain():
+    """ops/gemm.py:146-157 restated step by step in float64 / numpy: hidden = bf16(x W1^T); bf16(gelu(hidden + b1));
+    static E4M3 with the hidden exponents; bf16(. W2^T). b1 enters before the GELU: adding it after fails the bar."""
+    g = torch.Generator().manual_seed(2)
+    x = (torch.randn(64, 64, generator=g) * 4).to(torch.float8_e4m3fn)
+    xe = torch.tensor([-3, -2], dtype=torch.int8)  # one static exponent per 32 channels, shared by the rows
+    xd = x.double() * torch.exp2(xe.double()).repeat_interleave(32)
+    w1, w1e, w1d = _mx_operand(256, 64, 3)
+    w2, w2e, w2d = _mx_operand(64, 256, 4)
+    w1e, w2e = w1e.clamp(-7, -5), w2e.clamp(-7, -5)
+    w1d = w1.double() * torch.exp2(w1e.double()).repeat_interleave(32, dim=1)
+    w2d = w2.double() * torch.exp2(w2e.double()).repeat_interleave(32, dim=1)
+    b1 = torch.randn(256, generator=g)
+    he = torch.full((8,), -6, dtype=torch.int8)
+    got = ref.mxfp8_gelu_mlp(x, xe, w1, w1e, b1, he, w2, w2e).double()
+
+    def chain(bias_first: bool) -> torch.Tensor:
+        hidden = _bf16_np((xd @ w1d.t()).numpy().astype(np.float32)).astype(np.float64)
+        act = _gelu64(hidden + b1.double().numpy()) if bias_first else _gelu64(hidden) + b1.double().numpy()
+        act = _bf16_np(act.astype(np.float32))
+        q = torch.from_numpy((act * 64).clip(-448, 448).astype(np.float32)).to(torch.float8_e4m3fn).double() / 64
+        return torch.from_numpy(_bf16_np((q @ w2d.t()).numpy().astype(np.float32))).double()
+
+    want = chain(True)
+    assert (got - want).norm() / want.norm() < 2e-3
+    wrong = chain(False)
+    assert (wrong - want).norm() / want.norm() > 5e-2
+
+
+@pytest.mark.parametrize("h,w", [(8, 10), (7, 9)])
+def test_int8_conv2d_maxpool_against_brute_force_window_max(h, w):
+    """ops/conv.py:209-222: the pooled codes are quantize(max over each 2x2 window of the BF16 conv output), odd
+    trailing rows and columns dropped."""
+    torch.manual_seed(7)
+    x = torch.randint(-127, 127, (2, h, w, 16), dtype=torch.int8)
+    wt = torch.randint(-127, 127, (24, 9 * 16), dtype=torch.int8)
+    args = (x, wt, torch.tensor(0.02), torch.rand(24) * 0.01, torch.randn(24), 3, 3, 1, 1, 1, 1, 1, 1)
+    out, pooled = ref.int8_conv2d_maxpool(*args, relu=True, out_scale=torch.tensor(0.05))
+    assert torch.equal(out, ref.int8_conv2d(*args, relu=True))
+    o = out.float().numpy()
+    want = np.empty((2, h // 2, w // 2, 24), np.float32)
+    for y2 in range(h // 2):
+        for x2 in range(w // 2):
+            want[:, y2, x2] = o[:, 2 * y2: 2 * y2 + 2, 2 * x2: 2 * x2 + 2].max(axis=(1, 2))
+    codes = np.clip(np.rint(want / np.float32(0.05)), -127, 127)
+    assert pooled.shape == want.shape and np.array_equal(pooled.numpy(), codes.astype(np.int8))
+
+
+def test_depthwise5x5_gelu_against_float64():
+    """The producer: BF16 depthwise conv (FP32 accumulate) + bias -> BF16 -> GELU in BF16 (-> the consumer's quantize),
+    against a float64 tap loop, float64 GELU, and BF16 roundings by bit manipulation."""
+    torch.manual_seed(8)
+    x = torch.randn(1, 32, 9, 12) * 2
+    wt = (torch.randn(25, 32) * 0.3).to(torch.bfloat16)
+    b = torch.randn(32)
+    xb = x.to(torch.bfloat16).double().numpy()[0]  # [C, H, W]
+    pad = np.pad(xb, ((0, 0), (2, 2), (2, 2)))
+    conv = np.zeros_like(xb)
+    wn = wt.double().numpy()
+    for ky in range(5):
+        for kx in range(5):
+            conv += wn[ky * 5 + kx][:, None, None] * pad[:, ky: ky + 9, kx: kx + 12]
+    conv += b.double().numpy()[:, None, None]
+    pre = _bf16_np(conv.astype(np.float32))
+    want = _bf16_np(_gelu64(pre.astype(np.float64)).astype(np.float32)).transpose(1, 2, 0).reshape(-1, 32)
+    got = ref.depthwise5x5_gelu(x, wt, b).float().numpy()
+    step = np.maximum(np.abs(want), 2.0**-126) * 2.0**-7
+    # torch's CPU GELU of a BF16 tensor uses a vectorized erf: one BF16 step apart on a few percent of the values
+    assert (np.abs(got - want) <= step + 2.0**-14).all() and (got != want).mean() < 0.1
+    q = ref.depthwise5x5_gelu(x, wt, b, scale=torch.tensor(0.02)).numpy()
+    assert np.abs(q - np.clip(np.rint(want / np.float32(0.02)), -127, 127)).max() <= 1
+
+
+def test_add_residual_against_numpy_including_narrow_residual():
+    """ops/conv.py:198-203: out + residual in FP32 over the residual's channels (a narrower residual leaves the other
+    channels unchanged), optional ReLU over all channels, then one BF16 rounding."""
+    torch.manual_seed(9)
+    out = torch.randn(2, 3, 4, 48).to(torch.bfloat16)
+    res = torch.randn(2, 3, 4, 40).to(torch.bfloat16)
+    for relu in (False, True):
+        got = ref.add_residual(out, res, relu).float().numpy()
+        s = out.float().numpy().copy()
+        s[..., :40] = s[..., :40] + res.float().numpy()
+        if relu:
+            s = np.maximum(s, 0)
+        assert np.array_equal(got, _bf16_np(s.astype(np.float32)))
+
+
+def test_int8_linear_epilogue_order_relu_gelu_residual():
+    """ops/gemm.py:88-98: FP32 dequant + bias, ReLU, BF16, GELU in BF16, then residual + out in BF16 (residual after
+    GELU: adding it first gives different bits)."""
+    torch.manual_seed(10)
+    a = torch.randint(-127, 127, (33, 64), dtype=torch.int8)
+    w = torch.randint(-127, 127, (24, 64), dtype=torch.int8)
+    a_s, w_s, bias = torch.tensor(0.004), torch.rand(24) * 0.01, torch.randn(24)
+    res = torch.randn(33, 24).to(torch.bfloat16)
+    got = ref.int8_linear(a, w, a_s, w_s, bias, relu=True, gelu=True, residual=res).float().numpy()
+    acc = (a.long() @ w.long().t()).numpy().astype(np.float32)
+    y = (acc * (np.float32(a_s.item()) * w_s.numpy()).astype(np.float32)).astype(np.float32) + bias.numpy()
+    y = _bf16_np(np.maximum(y, 0).astype(np.float32))
+    y = _bf16_np(_gelu64(y.astype(np.float64)).astype(np.float32))
+    want = _bf16_np((y + res.float().numpy()).astype(np.float32))
+    assert np.abs(got - want).max() <= np.abs(want).max() * 2**-7 and (got != want).mean() < 2e-2
+    wrong = _bf16_np(_gelu64((y + res.float().numpy()).astype(np.float64)).astype(np.float32))
+    assert (np.abs(wrong - want) > 0.05).mean() > 0.2
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_gelu_quantize_producers_against_float64(dtype):
+    """ops/quantize.py:63-74, 128-131: GELU in the value's dtype (with input_bias: FP32 GELU of the sum, rounded back)
+    then the pinned static quantizers."""
+    torch.manual_seed(11)
+    x = (torch.randn(40, 64) * 3).to(dtype)
+    bias = torch.randn(64)
+    e = torch.tensor([-6, -6], dtype=torch.int8)
+    for input_bias in (None, bias):
+        v = x.double().numpy() + (0 if input_bias is None else bias.double().numpy())
+        g = _gelu64(v).astype(np.float32)
+        if dtype == torch.bfloat16:
+            g = _bf16_np(g)
+        want = ref.quantize_static(torch.from_numpy(g).to(dtype), e).view(torch.uint8)
+        got = ref.gelu_quantize(x, e, input_bias=input_bias).view(torch.uint8)
+        assert (got != want).float().mean() < 1e-2
+        step = torch.from_numpy(g).abs().double() * 2**-3 * 64 + 2**-9
+        diff = (got.view(torch.float8_e4m3fn).double() - want.view(torch.float8_e4m3fn).double()).abs()
+        assert (diff <= step).all()
+    gi = ref.gelu_quantize_int8(x, torch.tensor(0.05)).numpy()
+    g = _gelu64(x.double().numpy()).astype(np.float32)
+    g = _bf16_np(g) if dtype == torch.bfloat16 else g
+    assert np.abs(gi - np.clip(np.rint(g / np.float32(0.05)), -127, 127)).max() <= 1
+
+
+def test_int8_linear_quantize_is_the_requantized_linear():
+    """ops/gemm.py:104-116: round_half_even(int8_linear(...) / out_scale) saturated, computed here in numpy."""
+    torch.manual_seed(12)
+    a = torch.randint(-127, 127, (50, 32), dtype=torch.int8)
+    w = torch.randint(-127, 127, (16, 32), dtype=torch.int8)
+    args = (a, w, torch.tensor(0.01), torch.rand(16) * 0.01, torch.randn(16).to(torch.bfloat16))
+    got = ref.int8_linear_quantize(*args, torch.tensor(0.3)).numpy()
+    lin = ref.int8_linear(*args).float().numpy()
+    assert np.array_equal(got, np.clip(np.rint(lin / np.float32(0.3)), -127, 127).astype(np.int8))
+
+
+def test_pointwise_composites_against_float64_on_the_producer_codes():
+    """ops/conv.py:93-138: each block is its producer's codes through the pinned GEMM; recomputed in float64 from the
+    dequantized codes (MXFP8) and exactly in int64 (INT8)."""
+    torch.manual_seed(13)
+    x = torch.randn(1, 64, 6, 7)
+    dw_w, dw_b = (torch.randn(25, 64) * 0.3).to(torch.bfloat16), torch.randn(64)
+    pw, pe, pwd = _mx_operand(64, 64, 14)
+    pb = torch.randn(64)
+    out = ref.depthwise5x5_relu_pointwise_mxfp8(x, dw_w, dw_b, pw, ref.swizzle_scales(pe), ref.exponent_to_e8m0(pe),
+                                                pb)
+    codes, swz = ref.depthwise5x5_relu_mxfp8(x, dw_w, dw_b)
+    deq = ref.dequantize_swizzled(codes, swz).double()
+    exact = (deq @ pwd.t() + pb.double()).reshape(1, 6, 7, 64).permute(0, 3, 1, 2)
+    mag = (deq.abs() @ pwd.abs().t() + pb.double().abs()).reshape(1, 6, 7, 64).permute(0, 3, 1, 2)
+    assert ((out.double() - exact).abs() <= exact.abs() * 2**-8 + mag * 2**-20).all()
+    w8 = torch.randint(-127, 127, (64, 64), dtype=torch.int8)
+    ws, s = torch.rand(64) * 0.01, torch.tensor(0.05)
+    out8 = ref.depthwise5x5_relu_pointwise_int8(x, dw_w, dw_b, w8, ws, pb, s).permute(0, 2, 3, 1).reshape(-1, 64)
+    q = ref.depthwise5x5_relu_int8(x, dw_w, dw_b, s)
+    acc = (q.long() @ w8.long().t()).numpy().astype(np.float32)
+    y = (acc * (np.float32(0.05) * ws.numpy()).astype(np.float32)).astype(np.float32) + pb.numpy()
+    assert np.array_equal(out8.float().numpy(), _bf16_np(y.astype(np.float32)))
 
 
 # -- golden fixtures ---------------------------------------------------------------------------------------------
