@@ -33,6 +33,7 @@ SIGNATURES: dict[str, list] = {
     "fim_quantize_mxfp8_dynamic": [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp],
     "fim_quantize_int8_rows": [_vp, _i32, _i64, _i64, _i64, _i32, _vp, _vp, _vp],
     "fim_calibrate_block32": [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp],
+    "fim_calibrate_block32_noalloc": [_vp, _i32, _i64, _i64, _i64, _vp, _vp],
     "fim_int8_conv2d": [
         _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i32,
         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,

@@ -5,6 +5,7 @@
 //   fim_quantize_mxfp8_dynamic per-(row, 32) MXFP8 (+ the 128x4 swizzled E8M0 scales)  quant/formats/mx.py:50-86
 //   fim_quantize_int8_rows     per-row INT8 weights / tokens   quant/formats/int8.py:19-27, ops/quantize.py:148-157
 //   fim_calibrate_block32      static exponents from an amax over rows  quant/formats/mx.py:41-47
+//   fim_calibrate_block32_noalloc  the same without a caller workspace (file-scope device scratch; no allocation)
 //
 // Inputs are 4-D [B, H, W, C] with element strides, so both a packed NHWC tensor and the NHWC view of NCHW memory are
 // read in place. Three read paths:
@@ -12,6 +13,8 @@
 //   * width-contiguous (sw == 1, the NCHW view): a 64-pixel x 64-channel tile transposed through LDS, so both the
 //     read (along W) and the write (along C) are coalesced;
 //   * anything else: one element per lane.
+#include <mutex>
+
 #include "common.h"
 
 namespace fim {
@@ -405,6 +408,61 @@ __global__ void block_exponent_kernel(const uint32_t* __restrict__ amax_bits, in
   if (i < groups) expo[i] = (int8_t)mx_exponent_from_amax(u2f(amax_bits[i]));
 }
 
+// The launch sequence of the static-exponent calibration: clear the per-block amax words (a kernel, not a memset, so
+// the sequence can be captured in a graph), one atomicMax per 32-channel block and row slab, then the exponent rule.
+static int calibrate_launch(const void* x, int dtype, int64_t rows, int64_t C, int64_t row_stride, uint32_t* workspace,
+                            int8_t* exponent, hipStream_t stream) {
+  const int64_t groups = (C + 31) / 32;
+  fill_u32<<<dim3((unsigned)cdiv(groups, 256)), dim3(256), 0, stream>>>(workspace, groups);
+  if (rows > 0) {
+    int64_t rows_per_block = 64;
+    int64_t yb = cdiv(rows, rows_per_block);
+    while (yb > 65535) {
+      rows_per_block *= 2;
+      yb = cdiv(rows, rows_per_block);
+    }
+    dim3 grid((unsigned)cdiv(C, 256), (unsigned)yb);
+    switch (dtype) {
+      case FIM_F32:
+        block_amax_kernel<FIM_F32><<<grid, dim3(256), 0, stream>>>(x, rows, C, row_stride, rows_per_block, workspace);
+        break;
+      case FIM_BF16:
+        block_amax_kernel<FIM_BF16><<<grid, dim3(256), 0, stream>>>(x, rows, C, row_stride, rows_per_block, workspace);
+        break;
+      default:
+        block_amax_kernel<FIM_F16><<<grid, dim3(256), 0, stream>>>(x, rows, C, row_stride, rows_per_block, workspace);
+        break;
+    }
+  }
+  block_exponent_kernel<<<dim3((unsigned)cdiv(groups, 256)), dim3(256), 0, stream>>>(workspace, groups, exponent);
+  return launch_status();
+}
+
+// Scratch of the allocation-free calibration entry point: the per-block amax words live in this file-scope device
+// array (every GPU the library runs on holds its own copy, 16 KiB, until the process ends). Its device address is
+// looked up once per device with that device current and cached; host code passes only that address to kernels.
+constexpr int64_t FIM_CALIBRATE_MAX_GROUPS = 4096;  // C <= 131072 channels
+static __device__ __align__(256) uint32_t scratch[FIM_CALIBRATE_MAX_GROUPS];
+constexpr int FIM_MAX_DEVICES = 64;
+static uint32_t* scratch_ptr[FIM_MAX_DEVICES];
+static std::mutex scratch_mutex;
+
+static int calibrate_scratch(uint32_t** ptr) {
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return (int)err;
+  if (device < 0 || device >= FIM_MAX_DEVICES) return FIM_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (scratch_ptr[device] == nullptr) {
+    void* addr = nullptr;
+    err = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return (int)err;
+    scratch_ptr[device] = static_cast<uint32_t*>(addr);
+  }
+  *ptr = scratch_ptr[device];
+  return FIM_OK;
+}
+
 }  // namespace fim
 
 using namespace fim;
@@ -500,31 +558,19 @@ int fim_quantize_int8_rows(const void* x, int dtype, int64_t rows, int64_t K, in
 int fim_calibrate_block32(const void* x, int dtype, int64_t rows, int64_t C, int64_t row_stride, uint32_t* workspace,
                           int8_t* exponent, hipStream_t stream) {
   if (x == nullptr || workspace == nullptr || exponent == nullptr || rows < 0 || C <= 0) return FIM_ERR_INVALID;
-  const int64_t groups = (C + 31) / 32;
-  fill_u32<<<dim3((unsigned)cdiv(groups, 256)), dim3(256), 0, stream>>>(workspace, groups);
-  if (rows > 0) {
-    int64_t rows_per_block = 64;
-    int64_t yb = cdiv(rows, rows_per_block);
-    while (yb > 65535) {
-      rows_per_block *= 2;
-      yb = cdiv(rows, rows_per_block);
-    }
-    dim3 grid((unsigned)cdiv(C, 256), (unsigned)yb);
-    switch (dtype) {
-      case FIM_F32:
-        block_amax_kernel<FIM_F32><<<grid, dim3(256), 0, stream>>>(x, rows, C, row_stride, rows_per_block, workspace);
-        break;
-      case FIM_BF16:
-        block_amax_kernel<FIM_BF16><<<grid, dim3(256), 0, stream>>>(x, rows, C, row_stride, rows_per_block, workspace);
-        break;
-      case FIM_F16:
-        block_amax_kernel<FIM_F16><<<grid, dim3(256), 0, stream>>>(x, rows, C, row_stride, rows_per_block, workspace);
-        break;
-      default: return FIM_ERR_UNSUPPORTED;
-    }
-  }
-  block_exponent_kernel<<<dim3((unsigned)cdiv(groups, 256)), dim3(256), 0, stream>>>(workspace, groups, exponent);
-  return launch_status();
+  if (dtype != FIM_F32 && dtype != FIM_BF16 && dtype != FIM_F16) return FIM_ERR_UNSUPPORTED;
+  return calibrate_launch(x, dtype, rows, C, row_stride, workspace, exponent, stream);
+}
+
+int fim_calibrate_block32_noalloc(const void* x, int dtype, int64_t rows, int64_t C, int64_t row_stride,
+                                  int8_t* exponent, hipStream_t stream) {
+  if (x == nullptr || exponent == nullptr || rows < 0 || C <= 0) return FIM_ERR_INVALID;
+  if (dtype != FIM_F32 && dtype != FIM_BF16 && dtype != FIM_F16) return FIM_ERR_UNSUPPORTED;
+  if ((C + 31) / 32 > FIM_CALIBRATE_MAX_GROUPS) return FIM_ERR_UNSUPPORTED;
+  uint32_t* workspace = nullptr;
+  const int status = calibrate_scratch(&workspace);
+  if (status != FIM_OK) return status;
+  return calibrate_launch(x, dtype, rows, C, row_stride, workspace, exponent, stream);
 }
 
 }  // extern "C"

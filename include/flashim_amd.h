@@ -77,6 +77,15 @@ int fim_quantize_int8_rows(const void* x, int dtype, int64_t rows, int64_t K, in
 int fim_calibrate_block32(const void* x, int dtype, int64_t rows, int64_t C, int64_t row_stride, uint32_t* workspace,
                           int8_t* exponent, hipStream_t stream);
 
+/* fim_calibrate_block32 without the caller's workspace: no counterpart in the reference. For callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the
+ * per-block amax words live in a file-scope device array of FIM_CALIBRATE_MAX_GROUPS (4096) words, so C <= 131072
+ * (larger C returns FIM_ERR_UNSUPPORTED). It runs on the calling thread's current device; every call on one device
+ * shares that device's array (cleared at the start of each call), so calls that overlap on one device race. */
+#define FIM_CALIBRATE_MAX_GROUPS 4096
+int fim_calibrate_block32_noalloc(const void* x, int dtype, int64_t rows, int64_t C, int64_t row_stride,
+                                  int8_t* exponent, hipStream_t stream);
+
 /* ---- implicit-GEMM convolutions ----------------------------------------------------------------------------- */
 
 /* INT8 conv2d, groups == 1: x int8 [B, H, W, Cin] packed; weight int8 [Cout, kh*kw*Cin] in (ky, kx, c) order;

@@ -71,6 +71,14 @@ def test_int8_linear_quantize_rejects_a_row_stride_below_n():
                                         None) == _lib.FIM_ERR_INVALID
 
 
+def test_noalloc_calibration_rejects_widths_past_its_scratch_without_a_gpu():
+    lib = _lib.load()
+    fake = 1 << 20
+    assert lib.fim_calibrate_block32_noalloc(fake, 0, 1, 131073, 131073, fake, None) == _lib.FIM_ERR_UNSUPPORTED
+    assert lib.fim_calibrate_block32_noalloc(None, 0, 1, 32, 32, fake, None) == _lib.FIM_ERR_INVALID
+    assert lib.fim_calibrate_block32_noalloc(fake, 7, 1, 32, 32, fake, None) == _lib.FIM_ERR_UNSUPPORTED
+
+
 # -- host build of the scalar numerics ---------------------------------------------------------------------------
 
 
