@@ -120,7 +120,8 @@ __device__ __forceinline__ int pixel_of_row(const ConvArgs& a, int m, int& img, 
 
 // Epilogue of one wavefront's MB x NB blocks of 16 x 16 outputs, straight from the accumulators: D[n][m] with
 // lane = pixel (lane & 15) of a 16-pixel block and 4 consecutive channels 4 (lane >> 4) + v of a 16-channel block, so
-// each store writes 4 channels of one pixel. row0: the wave's first GEMM row; n_tile0: the tile's first channel; nl0:
+// each store writes 4 channels of one pixel. mrow[j]: this lane's GEMM row in block j (M or more: no output);
+// n_tile0: the tile's first channel; nl0:
 // the wave's first channel within the tile (index into the per-channel operands ep_* staged in LDS).
 // Branch-free epilogue for the common case (no residual, no pooling, Cout % 16 == 0, output below 2 GiB): per
 // 16-pixel row block, all NB x 4 values of the lane are computed (their chains, GELU's above all, interleave) and then
@@ -132,7 +133,8 @@ __device__ __forceinline__ int pixel_of_row(const ConvArgs& a, int m, int& img, 
 // out-of-range handling as the stores.
 template <int KIND, int OUT, int MB, int NB, bool GELU, bool RES = false>
 __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
-                                                   const v4f (&acc_f)[NB][MB], int row0, int n_tile0, int nl0,
+                                                   const v4f (&acc_f)[NB][MB], const int (&mrow)[MB], int n_tile0,
+                                                   int nl0,
                                                    const float* ep_scale, const float* ep_bias, const float* ep_osc) {
   constexpr int ESZ = OUT == OUT_BF16 ? 2 : 1;
   const int lane = threadIdx.x & 63;
@@ -165,7 +167,7 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
   }
   float arow[MB];
 #pragma unroll
-  for (int j = 0; j < MB; ++j) arow[j] = row_scales ? a.a_scale_rows[min(row0 + j * 16 + (lane & 15), a.M - 1)] : 1.f;
+  for (int j = 0; j < MB; ++j) arow[j] = row_scales ? a.a_scale_rows[min(mrow[j], a.M - 1)] : 1.f;
   float cs[NB][4], cb[NB][4], osc[NB];
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
@@ -178,7 +180,7 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
   }
 #pragma unroll
   for (int j = 0; j < MB; ++j) {
-    const int m = row0 + j * 16 + (lane & 15);
+    const int m = mrow[j];
     typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
     u32x2 rv[NB];
     if constexpr (RES) {  // this row block's residual, in flight while its values are computed
@@ -254,29 +256,46 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
   }
 }
 
-template <int KIND, int OUT, int POOL, int MB, int NB>
-__device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc_i)[NB][MB], const v4f (&acc_f)[NB][MB],
-                                              int row0, int n_tile0, int nl0, const float* ep_scale,
-                                              const float* ep_bias, const float* ep_osc) {
-  // a residual in the output's own dense BF16 layout (the refiner blocks' contract convs) stays on the fast path
+// The fast epilogue's variants (GELU, dense residual) for lane rows mrow; the caller has checked conv_fast_ok.
+template <int KIND, int OUT, int MB, int NB>
+__device__ __forceinline__ void conv_epilogue_rows(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
+                                                   const v4f (&acc_f)[NB][MB], const int (&mrow)[MB], int n_tile0,
+                                                   int nl0, const float* ep_scale, const float* ep_bias,
+                                                   const float* ep_osc) {
+  if (a.residual != nullptr) {
+    if (a.gelu)
+      conv_epilogue_fast<KIND, OUT, MB, NB, true, true>(a, acc_i, acc_f, mrow, n_tile0, nl0, ep_scale, ep_bias, ep_osc);
+    else
+      conv_epilogue_fast<KIND, OUT, MB, NB, false, true>(a, acc_i, acc_f, mrow, n_tile0, nl0, ep_scale, ep_bias,
+                                                         ep_osc);
+  } else if (a.gelu) {
+    conv_epilogue_fast<KIND, OUT, MB, NB, true>(a, acc_i, acc_f, mrow, n_tile0, nl0, ep_scale, ep_bias, ep_osc);
+  } else {
+    conv_epilogue_fast<KIND, OUT, MB, NB, false>(a, acc_i, acc_f, mrow, n_tile0, nl0, ep_scale, ep_bias, ep_osc);
+  }
+}
+
+// Whether the fast epilogue applies: no residual or a BF16 residual laid out as the output (the refiner blocks'
+// contract convs), no pooling, Cout % 16 == 0, the output below 2 GiB.
+template <int OUT>
+__host__ __device__ __forceinline__ bool conv_fast_ok(const ConvArgs& a) {
   const bool res_dense = a.residual != nullptr && a.res_dtype == FIM_BF16 && a.res_channels == a.Cout && a.rs_c == 1 &&
                          a.rs_w == a.Cout && a.rs_h == (int64_t)a.Wo * a.Cout &&
                          a.rs_b == (int64_t)a.Ho * a.Wo * a.Cout && ((uintptr_t)a.residual & 7) == 0 &&
                          (int64_t)a.M * a.Cout * 2 < (int64_t)0x7fffffff;
-  if (!POOL && (a.residual == nullptr || res_dense) && (a.Cout & 15) == 0 &&
-      (int64_t)a.M * a.out_ld * (OUT == OUT_BF16 ? 2 : 1) < (int64_t)0x7fffffff) {
-    if (a.residual != nullptr) {
-      if (a.gelu)
-        conv_epilogue_fast<KIND, OUT, MB, NB, true, true>(a, acc_i, acc_f, row0, n_tile0, nl0, ep_scale, ep_bias,
-                                                          ep_osc);
-      else
-        conv_epilogue_fast<KIND, OUT, MB, NB, false, true>(a, acc_i, acc_f, row0, n_tile0, nl0, ep_scale, ep_bias,
-                                                           ep_osc);
-    } else if (a.gelu) {
-      conv_epilogue_fast<KIND, OUT, MB, NB, true>(a, acc_i, acc_f, row0, n_tile0, nl0, ep_scale, ep_bias, ep_osc);
-    } else {
-      conv_epilogue_fast<KIND, OUT, MB, NB, false>(a, acc_i, acc_f, row0, n_tile0, nl0, ep_scale, ep_bias, ep_osc);
-    }
+  return a.pool_out == nullptr && (a.residual == nullptr || res_dense) && (a.Cout & 15) == 0 &&
+         (int64_t)a.M * a.out_ld * (OUT == OUT_BF16 ? 2 : 1) < (int64_t)0x7fffffff;
+}
+
+template <int KIND, int OUT, int POOL, int MB, int NB>
+__device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc_i)[NB][MB], const v4f (&acc_f)[NB][MB],
+                                              int row0, int n_tile0, int nl0, const float* ep_scale,
+                                              const float* ep_bias, const float* ep_osc) {
+  if (!POOL && conv_fast_ok<OUT>(a)) {
+    int mrow[MB];
+#pragma unroll
+    for (int j = 0; j < MB; ++j) mrow[j] = row0 + j * 16 + (threadIdx.x & 15);
+    conv_epilogue_rows<KIND, OUT, MB, NB>(a, acc_i, acc_f, mrow, n_tile0, nl0, ep_scale, ep_bias, ep_osc);
     return;
   }
   const int lane = threadIdx.x & 63;
@@ -996,6 +1015,352 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
                                       ep_osc);
 }
 
+// ---- Patch tiles -----------------------------------------------------------------------------------------------
+// Stride-1, dilation-1 3 x 3 convolutions with Cin == 128 (each of the 9 K steps is one tap's 128 channels).
+// Persistent workgroups of 4 wavefronts (one per SIMD, so each may hold 512 registers), one per CU, walk tiles of
+// TH x TW output pixels of one image x 64 output channels; wavefront w owns tile pixels [80 w, 80 w + 80) in row-major
+// order x the 64 channels: 5 x 4 blocks of 16 x 16.
+// * The workgroup's 64 output channels of the weights (9 taps x 64 x 128 B = 72 KB) stay in LDS for all its tiles
+//   (tiles are dealt so a workgroup keeps one channel block), with their MX exponents packed into registers.
+// * Per tile the (TH + 2) x (TW + 2) x 128-byte input patch is staged in LDS once (wave-wide `buffer_load ... lds`,
+//   pixels outside the image read as zero) and every tap reads its operand rows from the patch at the tap's offset:
+//   each activation byte crosses L2 -> LDS once instead of once per tap.
+// * The K loop has no barrier and no global load: as a step's MFMAs are issued block by block, each block's operand
+//   registers are refilled from LDS with the next step's rows (and the next step's weight rows go to a second set). The next tile's patch loads are issued before the epilogue, so they land
+//   while the epilogue computes and its stores drain.
+// Patch and weight rows are 128 bytes, 16-byte slot s of row r (patch pixel / output channel) holding channel segment
+// s ^ ((r >> 1) & 7). The epilogue is the conv kernels' fast epilogue (same arithmetic per value).
+
+// s_waitcnt immediate (gfx9 encoding) for at most `vm` outstanding vector memory operations and no LDS/scalar ones:
+// vmcnt in bits 3:0 and 15:14, expcnt (7: no wait) in 6:4, lgkmcnt (0) in 11:8. Issued through the builtin, so the
+// compiler's own wait counting sees it.
+constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 0xF) | (0x7 << 4) | (((vm >> 4) & 0x3) << 14); }
+
+template <int KIND, int OUT, int TH, int TW>
+__global__ __launch_bounds__(512, 1) void conv_patch_kernel(const ConvArgs a) {
+  constexpr int KW = 3, TAPS = 9, MB = 5, NB = 2, BN = 64;
+  // patch rows TW + 2 pixels wide, PW apart: a multiple of 16 pixels, so a tap's row offset keeps every pixel's
+  // swizzle and the operand addresses of the 9 taps are 3 column-offset sets plus constant row offsets
+  constexpr int PW = (TW + 2 + 15) / 16 * 16, NP = (TH + 2) * PW;
+  constexpr int PCHUNKS = (NP + 7) / 8;       // 8 patch pixels per wave-wide 1 KB load
+  constexpr int PCPW = (PCHUNKS + 7) / 8;     // patch loads per wavefront (at most)
+  constexpr int WCPW = TAPS * BN / 8 / 8;     // weight loads per wavefront: 9
+  constexpr int EPI_STORES = MB * NB;         // vector memory stores of one epilogue per wavefront
+  static_assert(4 * MB * 16 >= TH * TW, "four wavefronts of MB blocks cover the tile");
+  // one LDS block with fixed offsets, the patch at LDS address 0: a patch operand read is the lane's column offset
+  // plus the tap's row offset as the instruction's immediate (16-bit) offset, with no per-tap address registers
+  constexpr int WTS_BYTES = TAPS * BN * KC, PATCH_BYTES = PCHUNKS * 1024;
+  constexpr int WEXP_BYTES = KIND == KIND_MX ? TAPS * 4 * BN : 16;
+  static_assert(2 * PW * KC < 65536, "tap row offsets fit the immediate");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[PATCH_BYTES + WTS_BYTES + WEXP_BYTES + 3 * BN * 4 + 16];
+  uint8_t* const patch = smem;                           // [patch pixel][128 B]
+  uint8_t* const wts = smem + PATCH_BYTES;               // [tap][channel][128 B]
+  uint8_t* const wexp_s = wts + WTS_BYTES;               // [tap][block][channel] (MXFP8)
+  float* const ep_scale = reinterpret_cast<float*>(wexp_s + WEXP_BYTES);
+  float* const ep_bias = ep_scale + BN;
+  float* const ep_osc = ep_bias + BN;
+  uint8_t* const xexp_s = reinterpret_cast<uint8_t*>(ep_osc + BN);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4;
+  const int wm = wave & 3, wn = wave >> 2;
+
+  const int tiles_x = (a.Wo + TW - 1) / TW, tiles_y = (a.Ho + TH - 1) / TH;
+  const int total = a.n_tiles * tiles_x * tiles_y * a.B;
+  // XCD-aware deal (workgroup p runs on XCD p % 8): each XCD takes contiguous runs of tiles; the grid is a multiple of
+  // the channel-block count, so every tile of a workgroup has the same channel block
+  const int per_xcd = gridDim.x >> 3;
+  const int first = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (first >= total) return;
+  const int n0 = (first % a.n_tiles) * BN;
+
+  const int x_nrec = __builtin_amdgcn_readfirstlane((int)((int64_t)a.B * a.H * a.W * KC));
+  const int w_nrec = __builtin_amdgcn_readfirstlane(a.Cout * TAPS * KC);
+  constexpr uint32_t OOB = 0x80000000u;
+
+  // weights: chunk k = wave + 8 i (i < 9) holds rows (tap k / 8, channels 8 (k % 8) .. + 8) at wts + 1024 k
+#pragma unroll
+  for (int i = 0; i < WCPW; ++i) {
+    const int k = wave + 8 * i;
+    const int tap = k >> 3, r = 8 * (k & 7) + (lane >> 3);
+    const int seg = (lane & 7) ^ ((r >> 1) & 7);
+    const uint32_t off = n0 + r < a.Cout ? (uint32_t)(((n0 + r) * TAPS + tap) * KC + seg * 16) : OOB;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), (short)0, w_nrec, 0x00020000),
+        (lds_void_t*)(wts + k * 1024), 16, off, 0, 0, 0);
+  }
+  if (tid < BN) {
+    const int n = n0 + tid;
+    const bool nok = n < a.Cout;
+    ep_scale[tid] = (KIND == KIND_INT8 && nok) ? *a.a_scale * a.w_scale[n] : 1.0f;
+    float bias = -0.0f;
+    if (a.bias != nullptr && nok)
+      bias = a.bias_dtype == FIM_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(a.bias)[n])
+                                      : static_cast<const float*>(a.bias)[n];
+    ep_bias[tid] = bias;
+    ep_osc[tid] = (OUT == OUT_E4M3 && nok) ? exp2_int((int)a.out_expo[n >> 5]) : 1.0f;
+  }
+  if constexpr (KIND == KIND_MX) {
+    for (int idx = tid; idx < TAPS * 4 * BN; idx += 512) {  // E8M0 bytes of the weight rows (past Cout: 2^0)
+      const int kb = idx / BN, nl = idx - kb * BN;
+      const int n = n0 + nl;
+      wexp_s[idx] = (uint8_t)(n < a.Cout ? (int)a.w_expo[(int64_t)n * (TAPS * 4) + kb] + 127 : 127);
+    }
+    if (tid < 4) xexp_s[tid] = (uint8_t)((int)a.x_expo[tid] + 127);
+  }
+
+  // operand rows: this wavefront's pixel blocks as patch pixels at tap (0, 0), and the weight rows of its blocks
+  int qb[MB];
+#pragma unroll
+  for (int j = 0; j < MB; ++j) {
+    int p = wm * (MB * 16) + j * 16 + (lane & 15);
+    p = p < TH * TW ? p : 0;
+    qb[j] = (p / TW) * PW + (p % TW);
+  }
+  int fr_w[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int r = wn * (NB * 16) + i * 16 + (lane & 15);
+    fr_w[i] = r * KC + ((g ^ ((r >> 1) & 7)) << 4);
+  }
+
+  auto tile_origin = [&](int t, int& img, int& oy0, int& ox0) __attribute__((always_inline)) {
+    int rest = t / a.n_tiles;
+    ox0 = (rest % tiles_x) * TW;
+    rest /= tiles_x;
+    oy0 = (rest % tiles_y) * TH;
+    img = rest / tiles_y;
+  };
+  auto load_patch = [&](int t) __attribute__((always_inline)) {
+    int img, oy0, ox0;
+    tile_origin(t, img, oy0, ox0);
+    // recomputed per tile from the lane index (opaque to the compiler): hoisting the 2 x PCPW per-lane pixel
+    // coordinates out of the tile loop would cost more registers than it saves
+    int lid = lane;
+    asm volatile("" : "+v"(lid));
+#pragma unroll
+    for (int i = 0; i < PCPW; ++i) {
+      const int c = wave + 8 * i;
+      if (c < PCHUNKS) {
+        const int q = 8 * c + (lid >> 3);
+        const int seg = (lid & 7) ^ ((q >> 1) & 7);
+        const int iy = oy0 - a.ph + q / PW, ix = ox0 - a.pw + q % PW;
+        const bool ok = q % PW < TW + 2 && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
+        const uint32_t off = ok ? (uint32_t)(((img * a.H + iy) * a.W + ix) * KC + seg * 16) : OOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.x), (short)0, x_nrec, 0x00020000),
+            (lds_void_t*)(patch + c * 1024), 16, off, 0, 0, 0);
+      }
+    }
+  };
+  // LDS byte offsets of this lane's operand rows at tap column dx (row dy adds dy * PW rows): K pieces g and g + 4
+  int pofs[KW][MB][2];
+#pragma unroll
+  for (int dx = 0; dx < KW; ++dx)
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const int q = qb[j] + dx;
+      pofs[dx][j][0] = q * KC + ((g ^ ((q >> 1) & 7)) << 4);
+      pofs[dx][j][1] = pofs[dx][j][0] ^ 64;
+    }
+  // MFMA operands: block j's activation rows of tap kt from the patch at the tap's offset; the tap's weight rows
+  auto read_x = [&](int kt, int j, v8i& xf) __attribute__((always_inline)) {
+    const uint8_t* prow = patch + (kt / KW) * PW * KC;
+    const v4i lo = *reinterpret_cast<const v4i*>(prow + pofs[kt % KW][j][0]);
+    const v4i hi = *reinterpret_cast<const v4i*>(prow + pofs[kt % KW][j][1]);
+    xf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+  // the weight rows' LDS offsets, made opaque once per tile: the weights never change, and the compiler would
+  // otherwise hoist all 9 taps' weight operands out of the tile loop into registers it does not have
+  int fw[NB][2];
+  auto read_w = [&](int kt, v8i (&wf)[NB]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const v4i lo = *reinterpret_cast<const v4i*>(smem + fw[i][0] + kt * (BN * KC));
+      const v4i hi = *reinterpret_cast<const v4i*>(smem + fw[i][1] + kt * (BN * KC));
+      wf[i] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+  };
+
+  v4i acc_i[NB][MB];
+  v4f acc_f[NB][MB];
+  // MXFP8 scales in registers for every tile: the lane's activation block g, and per tap one dword of the E8M0 bytes
+  // of its NB weight rows (the MFMA's op_sel picks byte i)
+  int sx = 127, swp[TAPS];
+  v8i xf[MB], wa[NB], wb[NB];
+  // tap kt on the activation operands in xf and the weight operands in wc; as each block's MFMAs are issued, its
+  // registers are refilled with tap kt + 1's rows (a whole step of MFMAs away from their use), and tap kt + 1's weight
+  // rows go to wn first
+  auto step = [&](int kt, const v8i (&wc)[NB], v8i (&wn)[NB]) __attribute__((always_inline)) {
+    if (kt + 1 < TAPS) read_w(kt + 1, wn);
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      if constexpr (KIND == KIND_INT8) {
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+          acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_shufflevector(wc[i], wc[i], 0, 1, 2, 3),
+                                                              __builtin_shufflevector(xf[j], xf[j], 0, 1, 2, 3),
+                                                              acc_i[i][j], 0, 0, 0);
+          acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_shufflevector(wc[i], wc[i], 4, 5, 6, 7),
+                                                              __builtin_shufflevector(xf[j], xf[j], 4, 5, 6, 7),
+                                                              acc_i[i][j], 0, 0, 0);
+        }
+      } else {
+        acc_f[0][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wc[0], xf[j], acc_f[0][j], 0, 0, 0, swp[kt], 0, sx);
+        acc_f[1][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wc[1], xf[j], acc_f[1][j], 0, 0, 1, swp[kt], 0, sx);
+      }
+      if (kt + 1 < TAPS) read_x(kt + 1, j, xf[j]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  load_patch(first);
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));  // weights, the first patch, the staged operands
+  asm volatile("s_barrier" ::: "memory");
+  if constexpr (KIND == KIND_MX) {
+    sx = xexp_s[g];
+#pragma unroll
+    for (int t = 0; t < TAPS; ++t) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+        packed |= (uint32_t)wexp_s[(t * 4 + g) * BN + wn * (NB * 16) + i * 16 + (lane & 15)] << (8 * i);
+      swp[t] = (int)packed;
+    }
+  }
+
+  for (int t = first; t < total; t += gridDim.x) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int j = 0; j < MB; ++j) {
+        acc_i[i][j] = v4i{0, 0, 0, 0};
+        acc_f[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      fw[i][0] = PATCH_BYTES + fr_w[i];
+      fw[i][1] = PATCH_BYTES + (fr_w[i] ^ 64);
+      asm volatile("" : "+v"(fw[i][0]), "+v"(fw[i][1]));
+    }
+#pragma unroll
+    for (int j = 0; j < MB; ++j) read_x(0, j, xf[j]);
+    read_w(0, wa);
+    __builtin_amdgcn_sched_barrier(0);
+    step(0, wa, wb);
+    step(1, wb, wa);
+    step(2, wa, wb);
+    step(3, wb, wa);
+    step(4, wa, wb);
+    step(5, wb, wa);
+    step(6, wa, wb);
+    step(7, wb, wa);
+    step(8, wa, wb);
+    // the accumulators pinned here: left free, the MFMAs would be sunk past the barrier and patch loads below, next to
+    // their use in the epilogue, and every operand they read would stay live until then
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int j = 0; j < MB; ++j) {
+        if constexpr (KIND == KIND_INT8)
+          asm volatile("" : "+v"(acc_i[i][j]));
+        else
+          asm volatile("" : "+v"(acc_f[i][j]));
+      }
+    // every wavefront has read the patch for the last time: the next tile's patch loads go out before the epilogue
+    const int next = t + (int)gridDim.x;
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
+    asm volatile("s_barrier" ::: "memory");
+    if (next < total) load_patch(next);
+
+    int img, oy0, ox0;
+    tile_origin(t, img, oy0, ox0);
+    int mrow[MB];
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const int p = wm * (MB * 16) + j * 16 + (lane & 15);
+      const int oy = oy0 + p / TW, ox = ox0 + p % TW;
+      mrow[j] = (p < TH * TW && oy < a.Ho && ox < a.Wo) ? (img * a.Ho + oy) * a.Wo + ox : a.M;
+    }
+    // the per-channel operands re-read from LDS for every tile (opaque pointers): kept live across the tile loop, they
+    // would take registers the K loop needs
+    const float *eps = ep_scale, *epb = ep_bias, *epo = ep_osc;
+    asm volatile("" : "+v"(eps), "+v"(epb), "+v"(epo));
+    conv_epilogue_rows<KIND, OUT, MB, NB>(a, acc_i, acc_f, mrow, n0, wn * (NB * 16), eps, epb, epo);
+    if (next < total) {  // the patch loads precede the epilogue's stores, which may stay in flight
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(EPI_STORES));
+      asm volatile("s_barrier" ::: "memory");
+    }
+  }
+}
+
+// Patch-tile shapes (TH x TW output pixels, at most 320): the one whose tiles need the fewest per workgroup (the grid
+// holds at most one workgroup per CU), then the least halo. Returns the index into the launch table or -1 when the
+// patch kernel does not apply.
+struct PatchShape { int th, tw; };
+constexpr PatchShape PATCH_SHAPES[] = {{8, 40}, {16, 20}, {10, 32}};
+
+static int64_t patch_grid(int64_t tiles, int64_t n_tiles) {
+  // a multiple of 8 (XCDs) and of the channel-block count (each workgroup keeps one), at most one per CU
+  int64_t x = 8, y = n_tiles;
+  while (y != 0) {
+    const int64_t r = x % y;
+    x = y;
+    y = r;
+  }
+  const int64_t unit = 8 * n_tiles / x;
+  const int64_t cap = std::max<int64_t>(unit, device_cus() / unit * unit);
+  return std::min<int64_t>(cdiv(tiles, unit) * unit, cap);
+}
+
+static int patch_shape(const ConvArgs& a, int lw, bool fast_ok) {
+  if (lw != 16 || !fast_ok || a.x_swz != nullptr || a.pool_out != nullptr || a.a_scale_rows != nullptr) return -1;
+  if (a.Cin != KC || a.kh != 3 || a.kw != 3 || a.sh != 1 || a.sw != 1 || a.dh != 1 || a.dw != 1) return -1;
+  if ((int64_t)a.B * a.H * a.W * a.Cin >= (1LL << 31) - 16 || (int64_t)a.Cout * a.kh * a.kw * a.Cin >= (1LL << 31))
+    return -1;
+  const int64_t n_tiles = cdiv(a.Cout, 64);
+  int best = -1;
+  int64_t best_cost = 0, best_halo = 0;
+  for (int i = 0; i < (int)(sizeof(PATCH_SHAPES) / sizeof(PATCH_SHAPES[0])); ++i) {
+    const PatchShape sh = PATCH_SHAPES[i];
+    const int64_t tiles = (int64_t)a.B * cdiv(a.Ho, sh.th) * cdiv(a.Wo, sh.tw) * n_tiles;
+    if (tiles >= (1LL << 30)) continue;
+    const int64_t cost = cdiv(tiles, patch_grid(tiles, n_tiles)) * sh.th * sh.tw;  // tiles per workgroup x pixels
+    const int64_t halo = (int64_t)(sh.th + 2) * (sh.tw + 2);
+    if (best < 0 || cost < best_cost || (cost == best_cost && halo < best_halo)) {
+      best = i;
+      best_cost = cost;
+      best_halo = halo;
+    }
+  }
+  return best;
+}
+
+template <int KIND, int OUT>
+static void launch_patch_out(const ConvArgs& a, int shape, dim3 grid, hipStream_t stream) {
+  switch (shape) {
+    case 0: conv_patch_kernel<KIND, OUT, 8, 40><<<grid, dim3(512), 0, stream>>>(a); break;
+    case 1: conv_patch_kernel<KIND, OUT, 16, 20><<<grid, dim3(512), 0, stream>>>(a); break;
+    default: conv_patch_kernel<KIND, OUT, 10, 32><<<grid, dim3(512), 0, stream>>>(a); break;
+  }
+}
+
+template <int KIND>
+static int launch_patch(ConvArgs a, int shape, hipStream_t stream) {
+  const PatchShape sh = PATCH_SHAPES[shape];
+  a.n_tiles = (int)cdiv(a.Cout, 64);
+  const int64_t tiles = (int64_t)a.B * cdiv(a.Ho, sh.th) * cdiv(a.Wo, sh.tw) * a.n_tiles;
+  const dim3 grid((unsigned)patch_grid(tiles, a.n_tiles));
+  constexpr int QOUT = KIND == KIND_INT8 ? OUT_INT8 : OUT_E4M3;
+  if (a.out_mode == OUT_BF16)
+    launch_patch_out<KIND, OUT_BF16>(a, shape, grid, stream);
+  else
+    launch_patch_out<KIND, QOUT>(a, shape, grid, stream);
+  return launch_status();
+}
+
 template <int KIND, int WM>
 static void launch_wide(const ConvArgs& a, dim3 grid, hipStream_t stream) {
   constexpr int QOUT = KIND == KIND_INT8 ? OUT_INT8 : OUT_E4M3;
@@ -1117,6 +1482,8 @@ static int launch_conv(ConvArgs a, hipStream_t stream) {
   if (tiles > (1LL << 30)) return FIM_ERR_UNSUPPORTED;
   a.m_tiles = (int)m_tiles;
   a.m_base = 0;
+  const bool fast_ok = a.out_mode == OUT_BF16 ? conv_fast_ok<OUT_BF16>(a) : conv_fast_ok<OUT_INT8>(a);
+  if (const int shape = patch_shape(a, lw, fast_ok); shape >= 0) return launch_patch<KIND>(a, shape, stream);
   if (const int wm = wide_wm(a, lw)) {
     a.n_tiles = (int)cdiv((int64_t)a.Cout, (8 / wm) * 64);
     a.m_tiles = (int)cdiv((int64_t)a.M, wm * 80);

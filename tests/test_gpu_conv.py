@@ -415,3 +415,59 @@ def test_single_k_step_kernel_quantized_outputs(kind):
         out_exponent = torch.tensor([-2, -1, 0, 1], dtype=torch.int8)
         got_q = run(out_exponent=out_exponent.to(DEV))
         assert torch.equal(got_q.view(torch.uint8), ref.quantize_static(got, out_exponent).view(torch.uint8))
+
+
+# (name, image (B, H, W), Cin, Cout, geometry): shapes the patch-tile kernel takes (3 x 3, stride 1, dilation 1,
+# Cin == 128): partial tiles at the image edges, a partial channel block, several channel blocks and images (the
+# workgroups walk several tiles each), padding 0 and 2
+PATCH_CASES = [
+    ("3x3_edges", (1, 37, 45), 128, 128, (3, 3, 1, 1, 1, 1, 1, 1)),
+    ("3x3_n96_b2", (2, 19, 50), 128, 96, (3, 3, 1, 1, 1, 1, 1, 1)),
+    ("3x3_pad0", (1, 33, 41), 128, 48, (3, 3, 1, 1, 0, 0, 1, 1)),
+    ("3x3_n256_many_tiles", (3, 64, 120), 128, 256, (3, 3, 1, 1, 1, 1, 1, 1)),
+    ("3x3_pad2", (1, 20, 30), 128, 64, (3, 3, 1, 1, 2, 2, 1, 1)),
+]
+
+
+@pytest.mark.parametrize("case", range(len(PATCH_CASES)))
+def test_int8_conv2d_patch_tiles(case):
+    """INT8 through the patch-tile kernel: bit-exact BF16 out (bias + ReLU), with a dense residual, and INT8 out."""
+    name, shape, cin, cout, geo = PATCH_CASES[case]
+    x, weight, a_scale, w_scale, bias = _int8_inputs(cin, cout, geo[0], geo[1], True, shape=shape)
+    args = _dev(x, weight, a_scale, w_scale, bias)
+    hip = ops.int8_conv2d.get("hip")
+    got = hip(*args, *geo, relu=True).cpu()
+    want = ref.int8_conv2d(x, weight, a_scale, w_scale, bias, *geo, relu=True)
+    assert torch.equal(got, want), name
+    res = (torch.randn(*want.shape) * 4).to(torch.bfloat16)
+    got_r = hip(*args, *geo, relu=True, residual=res.to(DEV)).cpu()
+    assert torch.equal(got_r, ref.int8_conv2d(x, weight, a_scale, w_scale, bias, *geo, relu=True, residual=res)), name
+    out_scale = torch.tensor(0.09)
+    got_q = hip(*args, *geo, out_scale=out_scale.to(DEV)).cpu()
+    assert torch.equal(got_q, ref.int8_conv2d(x, weight, a_scale, w_scale, bias, *geo, out_scale=out_scale)), name
+
+
+@pytest.mark.parametrize("case", range(len(PATCH_CASES)))
+def test_mxfp8_conv2d_patch_tiles(case):
+    """MXFP8 through the patch-tile kernel: the oracle bar (plain, GELU within one BF16 step), and the E4M3 output
+    byte-identical to quantizing the kernel's own BF16 output."""
+    name, shape, cin, cout, geo = PATCH_CASES[case]
+    torch.manual_seed(case)
+    x = (torch.randn(*shape, cin) * 3).to(torch.float8_e4m3fn)
+    ce = torch.randint(-6, 3, (cin // 32,), dtype=torch.int8)
+    w = (torch.randn(cout, geo[0] * geo[1] * cin) * 2).to(torch.float8_e4m3fn)
+    we = torch.randint(-10, -4, (cout, geo[0] * geo[1] * cin // 32), dtype=torch.int8)
+    bias = torch.randn(cout).to(torch.bfloat16)
+    hip = ops.mxfp8_conv2d.get("hip")
+    args = _dev(x, ce, w, we, bias)
+    got = hip(*args, *geo).cpu()
+    want = ref.mxfp8_conv2d(x, ce, w, we, bias, *geo)
+    _assert_mx_close(got, want)
+    got_g = hip(*args, *geo, gelu=True).cpu().float()
+    want_g = ref.mxfp8_conv2d(x, ce, w, we, bias, *geo, gelu=True).float()
+    assert (got_g - want_g).norm() / want_g.norm() <= 1e-3, name
+    if cout % 32 == 0:
+        oe = torch.full((cout // 32,), -1, dtype=torch.int8)
+        got_q = hip(*args, *geo, out_exponent=oe.to(DEV))
+        assert torch.equal(got_q.view(torch.uint8), ops.quantize_mxfp8(hip(*args, *geo), oe.to(DEV)).values
+                           .view(torch.uint8)), name
