@@ -131,11 +131,39 @@ __device__ __forceinline__ int pixel_of_row(const ConvArgs& a, int m, int& img, 
 // RES: a BF16 residual laid out as the output ([M, Cout] dense, so its element offset is the output's), added after
 // the activation with the conv semantics relu(y + r) (ops/conv.py:198-203): loaded per row block with the same
 // out-of-range handling as the stores.
-template <int KIND, int OUT, int MB, int NB, bool GELU, bool RES = false>
+// The lane's per-channel epilogue operands: for each of its NB channel blocks, the scale and bias of its 4 channels
+// and their output scale (the lane's 4 channels, aligned by 4, share one 32-channel scale block).
+template <int NB>
+struct EpiChannels {
+  float cs[NB][4], cb[NB][4], osc[NB];
+};
+
+template <int NB>
+__device__ __forceinline__ EpiChannels<NB> epi_channels(int nl0, const float* ep_scale, const float* ep_bias,
+                                                        const float* ep_osc) {
+  const int g = (threadIdx.x & 63) >> 4;
+  EpiChannels<NB> ch;
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int nl = nl0 + i * 16 + 4 * g;
+    const float4 cs4 = *reinterpret_cast<const float4*>(&ep_scale[nl]);
+    const float4 cb4 = *reinterpret_cast<const float4*>(&ep_bias[nl]);
+    ch.cs[i][0] = cs4.x; ch.cs[i][1] = cs4.y; ch.cs[i][2] = cs4.z; ch.cs[i][3] = cs4.w;
+    ch.cb[i][0] = cb4.x; ch.cb[i][1] = cb4.y; ch.cb[i][2] = cb4.z; ch.cb[i][3] = cb4.w;
+    ch.osc[i] = ep_osc[nl];
+  }
+  return ch;
+}
+
+// Staged output: the values go to an LDS tile instead of global memory, row (tile pixel) spix[j] of STAGE_RB bytes per
+// pixel, 16-byte slot s of row p at slot s ^ stage_swz(p) (the caller writes the tile out in whole lines).
+__device__ __forceinline__ int stage_swz(int p) { return (p >> 1) & 7; }
+
+template <int KIND, int OUT, int MB, int NB, bool GELU, bool RES = false, int STAGE_RB = 0>
 __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
                                                    const v4f (&acc_f)[NB][MB], const int (&mrow)[MB], int n_tile0,
-                                                   int nl0,
-                                                   const float* ep_scale, const float* ep_bias, const float* ep_osc) {
+                                                   int nl0, const EpiChannels<NB>& ch, uint8_t* stage = nullptr,
+                                                   const int* spix = nullptr) {
   constexpr int ESZ = OUT == OUT_BF16 ? 2 : 1;
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4;
@@ -168,16 +196,9 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
   float arow[MB];
 #pragma unroll
   for (int j = 0; j < MB; ++j) arow[j] = row_scales ? a.a_scale_rows[min(mrow[j], a.M - 1)] : 1.f;
-  float cs[NB][4], cb[NB][4], osc[NB];
-#pragma unroll
-  for (int i = 0; i < NB; ++i) {
-    const int nl = nl0 + i * 16 + 4 * g;
-    const float4 cs4 = *reinterpret_cast<const float4*>(&ep_scale[nl]);
-    const float4 cb4 = *reinterpret_cast<const float4*>(&ep_bias[nl]);
-    cs[i][0] = cs4.x; cs[i][1] = cs4.y; cs[i][2] = cs4.z; cs[i][3] = cs4.w;
-    cb[i][0] = cb4.x; cb[i][1] = cb4.y; cb[i][2] = cb4.z; cb[i][3] = cb4.w;
-    osc[i] = ep_osc[nl];  // the lane's 4 channels (aligned by 4) share one 32-channel scale block
-  }
+  const auto& cs = ch.cs;
+  const auto& cb = ch.cb;
+  const auto& osc = ch.osc;
 #pragma unroll
   for (int j = 0; j < MB; ++j) {
     const int m = mrow[j];
@@ -235,9 +256,18 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
       const bool nvalid = n_tile0 + nl0 + i * 16 < a.Cout;  // whole 16-channel block in or out (Cout % 16 == 0)
       // rows past M land past the buffer's end; invalid channel blocks are sent there too
       const uint32_t off = nvalid ? ((uint32_t)m * (uint32_t)a.out_ld + (uint32_t)nbase) * ESZ : 0x80000000u;
+      uint8_t* sd = nullptr;
+      if constexpr (STAGE_RB > 0) {
+        const int cb = (nl0 + i * 16 + 4 * g) * ESZ;  // the lane's bytes within the staged row
+        const int sl = ((cb >> 4) ^ stage_swz(spix[j])) & (STAGE_RB / 16 - 1);
+        sd = stage + spix[j] * STAGE_RB + sl * 16 + (cb & 15);
+      }
       if (OUT == OUT_BF16) {
         const uint32_t lo = pack_bf16x2(v[0], v[1]), hi = pack_bf16x2(v[2], v[3]);
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rsrc, (int)off, 0, 0);
+        if constexpr (STAGE_RB > 0)
+          *reinterpret_cast<u32x2*>(sd) = u32x2{lo, hi};
+        else
+          __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rsrc, (int)off, 0, 0);
       } else {
         uint32_t pk;
         if (OUT == OUT_INT8) {
@@ -247,7 +277,10 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
         } else {
           pk = e4m3x4_of_bf16(v[0], v[1], v[2], v[3], osc[i], 448.0f * osc[i]);  // rounds to BF16 first
         }
-        __builtin_amdgcn_raw_buffer_store_b32(pk, rsrc, (int)off, 0, 0);
+        if constexpr (STAGE_RB > 0)
+          *reinterpret_cast<uint32_t*>(sd) = pk;
+        else
+          __builtin_amdgcn_raw_buffer_store_b32(pk, rsrc, (int)off, 0, 0);
       }
     }
     // this row block's stores (all NB x 16 channels of 16 pixels: whole 128-byte lines of a BF16 output) go out before
@@ -260,19 +293,46 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
 template <int KIND, int OUT, int MB, int NB>
 __device__ __forceinline__ void conv_epilogue_rows(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
                                                    const v4f (&acc_f)[NB][MB], const int (&mrow)[MB], int n_tile0,
-                                                   int nl0, const float* ep_scale, const float* ep_bias,
-                                                   const float* ep_osc) {
+                                                   int nl0, const EpiChannels<NB>& ch) {
   if (a.residual != nullptr) {
     if (a.gelu)
-      conv_epilogue_fast<KIND, OUT, MB, NB, true, true>(a, acc_i, acc_f, mrow, n_tile0, nl0, ep_scale, ep_bias, ep_osc);
+      conv_epilogue_fast<KIND, OUT, MB, NB, true, true>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch);
     else
-      conv_epilogue_fast<KIND, OUT, MB, NB, false, true>(a, acc_i, acc_f, mrow, n_tile0, nl0, ep_scale, ep_bias,
-                                                         ep_osc);
+      conv_epilogue_fast<KIND, OUT, MB, NB, false, true>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch);
   } else if (a.gelu) {
-    conv_epilogue_fast<KIND, OUT, MB, NB, true>(a, acc_i, acc_f, mrow, n_tile0, nl0, ep_scale, ep_bias, ep_osc);
+    conv_epilogue_fast<KIND, OUT, MB, NB, true>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch);
   } else {
-    conv_epilogue_fast<KIND, OUT, MB, NB, false>(a, acc_i, acc_f, mrow, n_tile0, nl0, ep_scale, ep_bias, ep_osc);
+    conv_epilogue_fast<KIND, OUT, MB, NB, false>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch);
   }
+}
+
+// The same into an LDS staging tile (see conv_epilogue_fast's STAGE_RB).
+template <int KIND, int OUT, int MB, int NB, int STAGE_RB>
+__device__ __forceinline__ void conv_epilogue_rows_staged(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
+                                                          const v4f (&acc_f)[NB][MB], const int (&mrow)[MB],
+                                                          int n_tile0, int nl0, const EpiChannels<NB>& ch,
+                                                          uint8_t* stage, const int* spix) {
+  if (a.residual != nullptr) {
+    if (a.gelu)
+      conv_epilogue_fast<KIND, OUT, MB, NB, true, true, STAGE_RB>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch, stage, spix);
+    else
+      conv_epilogue_fast<KIND, OUT, MB, NB, false, true, STAGE_RB>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch, stage,
+                                                                   spix);
+  } else if (a.gelu) {
+    conv_epilogue_fast<KIND, OUT, MB, NB, true, false, STAGE_RB>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch, stage, spix);
+  } else {
+    conv_epilogue_fast<KIND, OUT, MB, NB, false, false, STAGE_RB>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch, stage,
+                                                                  spix);
+  }
+}
+
+template <int KIND, int OUT, int MB, int NB>
+__device__ __forceinline__ void conv_epilogue_rows(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
+                                                   const v4f (&acc_f)[NB][MB], const int (&mrow)[MB], int n_tile0,
+                                                   int nl0, const float* ep_scale, const float* ep_bias,
+                                                   const float* ep_osc) {
+  conv_epilogue_rows<KIND, OUT, MB, NB>(a, acc_i, acc_f, mrow, n_tile0, nl0,
+                                        epi_channels<NB>(nl0, ep_scale, ep_bias, ep_osc));
 }
 
 // Whether the fast epilogue applies: no residual or a BF16 residual laid out as the output (the refiner blocks'
@@ -1017,45 +1077,103 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
 
 // ---- Patch tiles -----------------------------------------------------------------------------------------------
 // Stride-1, dilation-1 3 x 3 convolutions with Cin == 128 (each of the 9 K steps is one tap's 128 channels).
-// Persistent workgroups of 4 wavefronts (one per SIMD, so each may hold 512 registers), one per CU, walk tiles of
-// TH x TW output pixels of one image x 64 output channels; wavefront w owns tile pixels [80 w, 80 w + 80) in row-major
-// order x the 64 channels: 5 x 4 blocks of 16 x 16.
+// Persistent workgroups of 8 wavefronts, one per CU, walk tiles of TH x TW (12 x 16) output pixels of one image x 64
+// output channels.
 // * The workgroup's 64 output channels of the weights (9 taps x 64 x 128 B = 72 KB) stay in LDS for all its tiles
 //   (tiles are dealt so a workgroup keeps one channel block), with their MX exponents packed into registers.
 // * Per tile the (TH + 2) x (TW + 2) x 128-byte input patch is staged in LDS once (wave-wide `buffer_load ... lds`,
 //   pixels outside the image read as zero) and every tap reads its operand rows from the patch at the tap's offset:
 //   each activation byte crosses L2 -> LDS once instead of once per tap.
-// * The K loop has no barrier and no global load: as a step's MFMAs are issued block by block, each block's operand
-//   registers are refilled from LDS with the next step's rows (and the next step's weight rows go to a second set). The next tile's patch loads are issued before the epilogue, so they land
-//   while the epilogue computes and its stores drain.
-// Patch and weight rows are 128 bytes, 16-byte slot s of row r (patch pixel / output channel) holding channel segment
-// s ^ ((r >> 1) & 7). The epilogue is the conv kernels' fast epilogue (same arithmetic per value).
+// * Two groups of four wavefronts work on alternate tiles, half a tile period apart: while one group's K loop keeps
+//   the matrix cores busy, the other group (one wavefront per SIMD as well) runs its previous tile's epilogue on the
+//   VALU, stages the output in LDS, writes it out in whole 128-byte lines and loads its next patch.
+// * The K loop has no barrier and no global load: the next tap's operand rows are read from LDS between the current
+//   tap's MFMAs.
+// The epilogue is the conv kernels' fast epilogue (same arithmetic per value).
+
+// LDS slots. ds_read_b128 serves a wavefront in four passes of 16 lanes (the lanes with equal bit 5 and equal parity
+// of bits 2..4 of the lane index) over 64 four-byte banks, i.e. 16 groups of 16 bytes: a pass is conflict-free when its
+// 16 addresses fall in 16 distinct groups. A 128-byte row r covers groups 8 (r % 2) .. + 8, its 16-byte slot s
+// group 8 (r % 2) + s.
+// Weight rows: channel segment s of output channel r sits in slot s ^ patch_swz(r); a wavefront's 16 consecutive
+// channels read conflict-free.
+__device__ __forceinline__ int patch_swz(int r) { return (r >> 1) & 7; }
+// Patch pixels (rows of 18 pixels): segment s of the pixel in column c sits in slot s ^ patch_col_swz(c), from a table
+// of 3-bit entries searched so that the reads of 16 consecutive columns starting at column 0, 1 or 2 (the three tap
+// columns), low and high K halves (slots s and s ^ 4), are conflict-free in every pass (and measured so).
+constexpr uint64_t PATCH_COL_SWZ = 0x27c980a7358f67ULL;
+__device__ __forceinline__ int patch_col_swz(int c) { return (int)((PATCH_COL_SWZ >> (3 * c)) & 7); }
 
 // s_waitcnt immediate (gfx9 encoding) for at most `vm` outstanding vector memory operations and no LDS/scalar ones:
 // vmcnt in bits 3:0 and 15:14, expcnt (7: no wait) in 6:4, lgkmcnt (0) in 11:8. Issued through the builtin, so the
 // compiler's own wait counting sees it.
 constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 0xF) | (0x7 << 4) | (((vm >> 4) & 0x3) << 14); }
 
+// s_waitcnt for at most n (wave-uniform, at most 15; larger waits for 15) outstanding vector memory operations
+__device__ __forceinline__ void wait_vm_at_most(int n) {
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0)); break;
+    case 1: __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(1)); break;
+    case 2: __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(2)); break;
+    case 3: __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(3)); break;
+    case 4: __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(4)); break;
+    case 5: __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(5)); break;
+    case 6: __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(6)); break;
+    case 7: __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(7)); break;
+    case 8: __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(8)); break;
+    case 9: __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(9)); break;
+    case 10: __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(10)); break;
+    case 11: __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(11)); break;
+    case 12: __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(12)); break;
+    case 13: __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(13)); break;
+    case 14: __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(14)); break;
+    default: __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(15)); break;
+  }
+}
+
+// Scaled MXFP8 MFMA with the A-operand scale taken from byte i (0..3, a constant after unrolling) of scale_a.
+__device__ __forceinline__ v4f mfma_scale_opsel(const v8i& a, const v8i& b, v4f c, int i, int scale_a, int scale_b) {
+  switch (i) {
+    case 0: return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, scale_a, 0, scale_b);
+    case 1: return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 1, scale_a, 0, scale_b);
+    case 2: return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 2, scale_a, 0, scale_b);
+    default: return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 3, scale_a, 0, scale_b);
+  }
+}
+
+// Two groups of four wavefronts (wavefront w in group w / 4 runs on SIMD w % 4, so each SIMD holds one wavefront of each
+// group) take alternate tiles in a two-phase software pipeline: in each phase one group runs a tile's K loop (MFMA and
+// LDS reads) while the other runs the epilogue of its previous tile (VALU, LDS staging, stores) and loads its next
+// patch, and a workgroup barrier ends the phase. Each group has its own patch buffer; wavefront w % 4 of a group owns
+// tile pixels [16 MB (w % 4), +16 MB) x the 64 channels.
 template <int KIND, int OUT, int TH, int TW>
 __global__ __launch_bounds__(512, 1) void conv_patch_kernel(const ConvArgs a) {
-  constexpr int KW = 3, TAPS = 9, MB = 5, NB = 2, BN = 64;
-  // patch rows TW + 2 pixels wide, PW apart: a multiple of 16 pixels, so a tap's row offset keeps every pixel's
-  // swizzle and the operand addresses of the 9 taps are 3 column-offset sets plus constant row offsets
-  constexpr int PW = (TW + 2 + 15) / 16 * 16, NP = (TH + 2) * PW;
-  constexpr int PCHUNKS = (NP + 7) / 8;       // 8 patch pixels per wave-wide 1 KB load
-  constexpr int PCPW = (PCHUNKS + 7) / 8;     // patch loads per wavefront (at most)
-  constexpr int WCPW = TAPS * BN / 8 / 8;     // weight loads per wavefront: 9
-  constexpr int EPI_STORES = MB * NB;         // vector memory stores of one epilogue per wavefront
-  static_assert(4 * MB * 16 >= TH * TW, "four wavefronts of MB blocks cover the tile");
-  // one LDS block with fixed offsets, the patch at LDS address 0: a patch operand read is the lane's column offset
-  // plus the tap's row offset as the instruction's immediate (16-bit) offset, with no per-tap address registers
-  constexpr int WTS_BYTES = TAPS * BN * KC, PATCH_BYTES = PCHUNKS * 1024;
+  constexpr int KW = 3, TAPS = 9, NB = 4, BN = 64;
+  constexpr int MB = TH * TW / 64;  // 16-pixel blocks per wavefront
+  static_assert(MB * 64 == TH * TW, "four wavefronts of MB blocks cover the tile");
+  // patch rows of PW = TW + 2 pixels; a 16-pixel block is one tile row, and the slot follows the column, so the operand
+  // addresses of the 9 taps are 3 column-offset sets plus constant row offsets
+  static_assert(TW == 16, "pixel blocks are tile rows, patch rows the 18 columns the slot table covers");
+  constexpr int PW = TW + 2, NP = (TH + 2) * PW;
+  constexpr int PCHUNKS = (NP + 7) / 8;          // wave-wide 1 KB loads of 8 patch pixels
+  constexpr int PATCH_BYTES = PCHUNKS * 1024;    // one patch buffer
+  constexpr int WTS_BYTES = TAPS * BN * KC;
   constexpr int WEXP_BYTES = KIND == KIND_MX ? TAPS * 4 * BN : 16;
+  // output staging: a wavefront's pixels in SROUNDS rounds of SPIX pixels, RB bytes (64 channels) each
+  constexpr int ESZ = OUT == OUT_BF16 ? 2 : 1;
+  constexpr int RB = BN * ESZ, LPP = RB / 16, PPC = 64 / LPP;
+  constexpr int SROUNDS = MB, SPIX = 16;          // one 16-pixel block per round
+  constexpr int SCH = SPIX / PPC;                // 1 KB stores per round
+  static_assert(SPIX % PPC == 0, "whole 1 KB stores per round");
+  constexpr int STAGE_BYTES = 4 * SPIX * RB;
+  // one LDS block with fixed offsets, the two patch buffers first: a patch operand read is the lane's column offset
+  // (plus the group's buffer) in a register and the tap-row offset as the instruction's 16-bit immediate
   static_assert(2 * PW * KC < 65536, "tap row offsets fit the immediate");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[PATCH_BYTES + WTS_BYTES + WEXP_BYTES + 3 * BN * 4 + 16];
-  uint8_t* const patch = smem;                           // [patch pixel][128 B]
-  uint8_t* const wts = smem + PATCH_BYTES;               // [tap][channel][128 B]
-  uint8_t* const wexp_s = wts + WTS_BYTES;               // [tap][block][channel] (MXFP8)
+  __shared__ __attribute__((aligned(1024)))
+  uint8_t smem[2 * PATCH_BYTES + WTS_BYTES + STAGE_BYTES + WEXP_BYTES + 3 * BN * 4 + 16];
+  uint8_t* const wts = smem + 2 * PATCH_BYTES;           // [tap][channel][128 B]
+  uint8_t* const stage = wts + WTS_BYTES;                // [wavefront % 4][pixel][RB]
+  uint8_t* const wexp_s = stage + STAGE_BYTES;           // [channel][tap][block] (MXFP8)
   float* const ep_scale = reinterpret_cast<float*>(wexp_s + WEXP_BYTES);
   float* const ep_bias = ep_scale + BN;
   float* const ep_osc = ep_bias + BN;
@@ -1065,16 +1183,23 @@ __global__ __launch_bounds__(512, 1) void conv_patch_kernel(const ConvArgs a) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4;
-  const int wm = wave & 3, wn = wave >> 2;
+  const int grp = wave >> 2, wq = wave & 3;
 
   const int tiles_x = (a.Wo + TW - 1) / TW, tiles_y = (a.Ho + TH - 1) / TH;
   const int total = a.n_tiles * tiles_x * tiles_y * a.B;
   // XCD-aware deal (workgroup p runs on XCD p % 8): each XCD takes contiguous runs of tiles; the grid is a multiple of
-  // the channel-block count, so every tile of a workgroup has the same channel block
-  const int per_xcd = gridDim.x >> 3;
+  // the channel-block count, so every tile of a workgroup has the same channel block. The workgroup's tiles are
+  // first, first + stride, ...; group q takes those with an even (q = 0) or odd (q = 1) index.
+  const int stride = gridDim.x;
+  const int per_xcd = stride >> 3;
   const int first = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
   if (first >= total) return;
   const int n0 = (first % a.n_tiles) * BN;
+  const int n_mine = (total - first + stride - 1) / stride;  // tiles of the workgroup
+  const int n_grp = (n_mine - grp + 1) >> 1;                 // ... of this group
+  // phases: the group's k-th tile runs its K loop in phase 2 k + grp and its epilogue in the phase after
+  const int n_phases = max(2 * ((n_mine + 1) >> 1), 2 * (n_mine >> 1) + 1);
+  uint8_t* const buf = smem + grp * PATCH_BYTES;
 
   const int x_nrec = __builtin_amdgcn_readfirstlane((int)((int64_t)a.B * a.H * a.W * KC));
   const int w_nrec = __builtin_amdgcn_readfirstlane(a.Cout * TAPS * KC);
@@ -1082,15 +1207,50 @@ __global__ __launch_bounds__(512, 1) void conv_patch_kernel(const ConvArgs a) {
 
   // weights: chunk k = wave + 8 i (i < 9) holds rows (tap k / 8, channels 8 (k % 8) .. + 8) at wts + 1024 k
 #pragma unroll
-  for (int i = 0; i < WCPW; ++i) {
+  for (int i = 0; i < TAPS * BN / 64; ++i) {
     const int k = wave + 8 * i;
     const int tap = k >> 3, r = 8 * (k & 7) + (lane >> 3);
-    const int seg = (lane & 7) ^ ((r >> 1) & 7);
+    const int seg = (lane & 7) ^ patch_swz(r);
     const uint32_t off = n0 + r < a.Cout ? (uint32_t)(((n0 + r) * TAPS + tap) * KC + seg * 16) : OOB;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), (short)0, w_nrec, 0x00020000),
         (lds_void_t*)(wts + k * 1024), 16, off, 0, 0, 0);
   }
+
+  auto tile_origin = [&](int t, int& img, int& oy0, int& ox0) __attribute__((always_inline)) {
+    int rest = t / a.n_tiles;
+    ox0 = (rest % tiles_x) * TW;
+    rest /= tiles_x;
+    oy0 = (rest % tiles_y) * TH;
+    img = rest / tiles_y;
+  };
+  // patch of tile t into this group's buffer: load i of the group's wavefront q brings patch pixels 8 (q + 4 i) .. + 8
+  // (pixels outside the image and past NP read as zero)
+  constexpr int PLOADS = (PCHUNKS + 3) / 4;
+  const int my_patch = (PCHUNKS - wq + 3) >> 2;  // this wavefront's loads per patch
+  auto load_patch = [&](int t) __attribute__((always_inline)) {
+    int img, oy0, ox0;
+    tile_origin(t, img, oy0, ox0);
+    int lid = lane;
+    asm volatile("" : "+v"(lid));  // per-lane coordinates recomputed per tile instead of held in registers
+#pragma unroll
+    for (int i = 0; i < PLOADS; ++i) {
+      const int c = wq + 4 * i;
+      if (c < PCHUNKS) {
+        const int q = 8 * c + (lid >> 3);
+        const int col = q % PW;
+        const int seg = (lid & 7) ^ patch_col_swz(col);
+        const int iy = oy0 - a.ph + q / PW, ix = ox0 - a.pw + col;
+        const bool ok = q < NP && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
+        const uint32_t off = ok ? (uint32_t)(((img * a.H + iy) * a.W + ix) * KC + seg * 16) : OOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.x), (short)0, x_nrec, 0x00020000),
+            (lds_void_t*)(buf + c * 1024), 16, off, 0, 0, 0);
+      }
+    }
+  };
+  if (grp < n_mine) load_patch(first + grp * stride);
+
   if (tid < BN) {
     const int n = n0 + tid;
     const bool nok = n < a.Cout;
@@ -1103,78 +1263,46 @@ __global__ __launch_bounds__(512, 1) void conv_patch_kernel(const ConvArgs a) {
     ep_osc[tid] = (OUT == OUT_E4M3 && nok) ? exp2_int((int)a.out_expo[n >> 5]) : 1.0f;
   }
   if constexpr (KIND == KIND_MX) {
-    for (int idx = tid; idx < TAPS * 4 * BN; idx += 512) {  // E8M0 bytes of the weight rows (past Cout: 2^0)
-      const int kb = idx / BN, nl = idx - kb * BN;
-      const int n = n0 + nl;
-      wexp_s[idx] = (uint8_t)(n < a.Cout ? (int)a.w_expo[(int64_t)n * (TAPS * 4) + kb] + 127 : 127);
+    // E8M0 bytes of the weight rows (past Cout: 2^0), one contiguous run of BN x 36 bytes: every load is issued
+    // before the first LDS store, so the prologue waits for one memory round trip, not one per pass
+    constexpr int WEXP_N = TAPS * 4 * BN, WEXP_PASSES = (WEXP_N + 511) / 512;
+    const int64_t wexp_valid = ((int64_t)a.Cout - n0) * (TAPS * 4);
+    int e[WEXP_PASSES];
+#pragma unroll
+    for (int i = 0; i < WEXP_PASSES; ++i) {
+      const int idx = tid + 512 * i;
+      e[i] = idx < WEXP_N && idx < wexp_valid ? (int)a.w_expo[(int64_t)n0 * (TAPS * 4) + idx] + 127 : 127;
     }
+#pragma unroll
+    for (int i = 0; i < WEXP_PASSES; ++i)
+      if (tid + 512 * i < WEXP_N) wexp_s[tid + 512 * i] = (uint8_t)e[i];
     if (tid < 4) xexp_s[tid] = (uint8_t)((int)a.x_expo[tid] + 127);
   }
 
-  // operand rows: this wavefront's pixel blocks as patch pixels at tap (0, 0), and the weight rows of its blocks
-  int qb[MB];
-#pragma unroll
-  for (int j = 0; j < MB; ++j) {
-    int p = wm * (MB * 16) + j * 16 + (lane & 15);
-    p = p < TH * TW ? p : 0;
-    qb[j] = (p / TW) * PW + (p % TW);
-  }
-  int fr_w[NB];
-#pragma unroll
-  for (int i = 0; i < NB; ++i) {
-    const int r = wn * (NB * 16) + i * 16 + (lane & 15);
-    fr_w[i] = r * KC + ((g ^ ((r >> 1) & 7)) << 4);
-  }
-
-  auto tile_origin = [&](int t, int& img, int& oy0, int& ox0) __attribute__((always_inline)) {
-    int rest = t / a.n_tiles;
-    ox0 = (rest % tiles_x) * TW;
-    rest /= tiles_x;
-    oy0 = (rest % tiles_y) * TH;
-    img = rest / tiles_y;
-  };
-  auto load_patch = [&](int t) __attribute__((always_inline)) {
-    int img, oy0, ox0;
-    tile_origin(t, img, oy0, ox0);
-    // recomputed per tile from the lane index (opaque to the compiler): hoisting the 2 x PCPW per-lane pixel
-    // coordinates out of the tile loop would cost more registers than it saves
-    int lid = lane;
-    asm volatile("" : "+v"(lid));
-#pragma unroll
-    for (int i = 0; i < PCPW; ++i) {
-      const int c = wave + 8 * i;
-      if (c < PCHUNKS) {
-        const int q = 8 * c + (lid >> 3);
-        const int seg = (lid & 7) ^ ((q >> 1) & 7);
-        const int iy = oy0 - a.ph + q / PW, ix = ox0 - a.pw + q % PW;
-        const bool ok = q % PW < TW + 2 && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
-        const uint32_t off = ok ? (uint32_t)(((img * a.H + iy) * a.W + ix) * KC + seg * 16) : OOB;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.x), (short)0, x_nrec, 0x00020000),
-            (lds_void_t*)(patch + c * 1024), 16, off, 0, 0, 0);
-      }
-    }
-  };
-  // LDS byte offsets of this lane's operand rows at tap column dx (row dy adds dy * PW rows): K pieces g and g + 4
-  int pofs[KW][MB][2];
+  // operand rows: this wavefront's pixel blocks as patch pixels at tap (0, 0) in its group's buffer, the weight rows
+  int pofs[KW][MB][2];  // LDS byte offsets at tap column dx (row dy adds dy * PW rows): K pieces g and g + 4
 #pragma unroll
   for (int dx = 0; dx < KW; ++dx)
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
-      const int q = qb[j] + dx;
-      pofs[dx][j][0] = q * KC + ((g ^ ((q >> 1) & 7)) << 4);
+      const int p = wq * (MB * 16) + j * 16 + (lane & 15);
+      const int q = (p / TW) * PW + (p % TW) + dx;
+      pofs[dx][j][0] = grp * PATCH_BYTES + q * KC + ((g ^ patch_col_swz(q % PW)) << 4);
       pofs[dx][j][1] = pofs[dx][j][0] ^ 64;
     }
-  // MFMA operands: block j's activation rows of tap kt from the patch at the tap's offset; the tap's weight rows
+  int fr_w[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int r = i * 16 + (lane & 15);
+    fr_w[i] = r * KC + ((g ^ patch_swz(r)) << 4);
+  }
+  int fw[NB][2];  // the weight offsets, made opaque per tile (else all 9 taps' weight rows are hoisted into registers)
   auto read_x = [&](int kt, int j, v8i& xf) __attribute__((always_inline)) {
-    const uint8_t* prow = patch + (kt / KW) * PW * KC;
+    const uint8_t* prow = smem + (kt / KW) * PW * KC;
     const v4i lo = *reinterpret_cast<const v4i*>(prow + pofs[kt % KW][j][0]);
     const v4i hi = *reinterpret_cast<const v4i*>(prow + pofs[kt % KW][j][1]);
     xf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   };
-  // the weight rows' LDS offsets, made opaque once per tile: the weights never change, and the compiler would
-  // otherwise hoist all 9 taps' weight operands out of the tile loop into registers it does not have
-  int fw[NB][2];
   auto read_w = [&](int kt, v8i (&wf)[NB]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
@@ -1187,37 +1315,10 @@ __global__ __launch_bounds__(512, 1) void conv_patch_kernel(const ConvArgs a) {
   v4i acc_i[NB][MB];
   v4f acc_f[NB][MB];
   // MXFP8 scales in registers for every tile: the lane's activation block g, and per tap one dword of the E8M0 bytes
-  // of its NB weight rows (the MFMA's op_sel picks byte i)
+  // of its 4 weight rows (the MFMA's op_sel picks byte i)
   int sx = 127, swp[TAPS];
-  v8i xf[MB], wa[NB], wb[NB];
-  // tap kt on the activation operands in xf and the weight operands in wc; as each block's MFMAs are issued, its
-  // registers are refilled with tap kt + 1's rows (a whole step of MFMAs away from their use), and tap kt + 1's weight
-  // rows go to wn first
-  auto step = [&](int kt, const v8i (&wc)[NB], v8i (&wn)[NB]) __attribute__((always_inline)) {
-    if (kt + 1 < TAPS) read_w(kt + 1, wn);
-#pragma unroll
-    for (int j = 0; j < MB; ++j) {
-      if constexpr (KIND == KIND_INT8) {
-#pragma unroll
-        for (int i = 0; i < NB; ++i) {
-          acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_shufflevector(wc[i], wc[i], 0, 1, 2, 3),
-                                                              __builtin_shufflevector(xf[j], xf[j], 0, 1, 2, 3),
-                                                              acc_i[i][j], 0, 0, 0);
-          acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_shufflevector(wc[i], wc[i], 4, 5, 6, 7),
-                                                              __builtin_shufflevector(xf[j], xf[j], 4, 5, 6, 7),
-                                                              acc_i[i][j], 0, 0, 0);
-        }
-      } else {
-        acc_f[0][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wc[0], xf[j], acc_f[0][j], 0, 0, 0, swp[kt], 0, sx);
-        acc_f[1][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wc[1], xf[j], acc_f[1][j], 0, 0, 1, swp[kt], 0, sx);
-      }
-      if (kt + 1 < TAPS) read_x(kt + 1, j, xf[j]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-
-  load_patch(first);
-  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));  // weights, the first patch, the staged operands
+  // the group's first patch, the weights and the staged operands
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
   asm volatile("s_barrier" ::: "memory");
   if constexpr (KIND == KIND_MX) {
     sx = xexp_s[g];
@@ -1226,12 +1327,15 @@ __global__ __launch_bounds__(512, 1) void conv_patch_kernel(const ConvArgs a) {
       uint32_t packed = 0;
 #pragma unroll
       for (int i = 0; i < NB; ++i)
-        packed |= (uint32_t)wexp_s[(t * 4 + g) * BN + wn * (NB * 16) + i * 16 + (lane & 15)] << (8 * i);
+        packed |= (uint32_t)wexp_s[(i * 16 + (lane & 15)) * (TAPS * 4) + t * 4 + g] << (8 * i);
       swp[t] = (int)packed;
     }
   }
 
-  for (int t = first; t < total; t += gridDim.x) {
+  // K loop of a tile: the activation rows of the next tap and the weight rows of the next tap are read while a tap's
+  // MFMAs are issued (two register sets each)
+  auto k_loop = [&]() __attribute__((always_inline)) {
+    v8i xs[2][MB], ws[2][NB];
 #pragma unroll
     for (int i = 0; i < NB; ++i)
 #pragma unroll
@@ -1241,25 +1345,52 @@ __global__ __launch_bounds__(512, 1) void conv_patch_kernel(const ConvArgs a) {
       }
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      fw[i][0] = PATCH_BYTES + fr_w[i];
-      fw[i][1] = PATCH_BYTES + (fr_w[i] ^ 64);
+      fw[i][0] = 2 * PATCH_BYTES + fr_w[i];
+      fw[i][1] = 2 * PATCH_BYTES + (fr_w[i] ^ 64);
       asm volatile("" : "+v"(fw[i][0]), "+v"(fw[i][1]));
     }
 #pragma unroll
-    for (int j = 0; j < MB; ++j) read_x(0, j, xf[j]);
-    read_w(0, wa);
-    __builtin_amdgcn_sched_barrier(0);
-    step(0, wa, wb);
-    step(1, wb, wa);
-    step(2, wa, wb);
-    step(3, wb, wa);
-    step(4, wa, wb);
-    step(5, wb, wa);
-    step(6, wa, wb);
-    step(7, wb, wa);
-    step(8, wa, wb);
-    // the accumulators pinned here: left free, the MFMAs would be sunk past the barrier and patch loads below, next to
-    // their use in the epilogue, and every operand they read would stay live until then
+    for (int j = 0; j < MB; ++j) read_x(0, j, xs[0][j]);
+    read_w(0, ws[0]);
+#pragma unroll
+    for (int kt = 0; kt < TAPS; ++kt) {
+      if (kt + 1 < TAPS) {
+#pragma unroll
+        for (int j = 0; j < MB; ++j) read_x(kt + 1, j, xs[(kt + 1) & 1][j]);
+        read_w(kt + 1, ws[(kt + 1) & 1]);
+      }
+      const v8i (&xf)[MB] = xs[kt & 1];
+      const v8i (&wc)[NB] = ws[kt & 1];
+#pragma unroll
+      for (int j = 0; j < MB; ++j)
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+          if constexpr (KIND == KIND_INT8) {
+            acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_shufflevector(wc[i], wc[i], 0, 1, 2, 3),
+                                                                __builtin_shufflevector(xf[j], xf[j], 0, 1, 2, 3),
+                                                                acc_i[i][j], 0, 0, 0);
+            acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_shufflevector(wc[i], wc[i], 4, 5, 6, 7),
+                                                                __builtin_shufflevector(xf[j], xf[j], 4, 5, 6, 7),
+                                                                acc_i[i][j], 0, 0, 0);
+          } else {
+            acc_f[i][j] = mfma_scale_opsel(wc[i], xf[j], acc_f[i][j], i, swp[kt], sx);
+          }
+        }
+      // one wavefront per SIMD runs the K loop: the next tap's LDS reads are issued one by one between this tap's
+      // MFMAs, in their shadow, instead of as a burst the matrix core waits behind
+      if (kt + 1 < TAPS) {
+        constexpr int NMFMA = MB * NB * (KIND == KIND_INT8 ? 2 : 1), NREAD = 2 * (MB + NB);
+#pragma unroll
+        for (int n = 0; n < NMFMA; ++n) {
+          if (n < NREAD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // one MFMA
+        }
+        if (NREAD > NMFMA) __builtin_amdgcn_sched_group_barrier(0x100, NREAD > NMFMA ? NREAD - NMFMA : 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // the accumulators pinned here: left free, the MFMAs would be sunk into the epilogue phase, and every operand they
+    // read would stay live until then
 #pragma unroll
     for (int i = 0; i < NB; ++i)
 #pragma unroll
@@ -1269,38 +1400,84 @@ __global__ __launch_bounds__(512, 1) void conv_patch_kernel(const ConvArgs a) {
         else
           asm volatile("" : "+v"(acc_f[i][j]));
       }
-    // every wavefront has read the patch for the last time: the next tile's patch loads go out before the epilogue
-    const int next = t + (int)gridDim.x;
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
-    asm volatile("s_barrier" ::: "memory");
-    if (next < total) load_patch(next);
+  };
 
+  // epilogue of tile t: first the loads of the group's next patch (its buffer is free: the K loop finished in the
+  // previous phase), then the values, staged per wavefront in rounds and written out in whole lines; at the end this
+  // wavefront's patch loads (issued before its stores) are waited for
+  const int nbytes = __builtin_amdgcn_readfirstlane((int)((uint32_t)a.M * (uint32_t)a.out_ld * ESZ));
+  auto epilogue = [&](int t, int next) __attribute__((always_inline)) {
+    if (next < total) load_patch(next);
+    int eo = 0;
+    asm volatile("" : "+v"(eo));  // the per-channel operands re-read from LDS per tile, not held across the K loop
+    const EpiChannels<NB> ch = epi_channels<NB>(0, ep_scale + eo, ep_bias + eo, ep_osc + eo);
     int img, oy0, ox0;
     tile_origin(t, img, oy0, ox0);
-    int mrow[MB];
+    const uint64_t out_addr = (uint64_t)a.out;
+    const uint64_t out_u = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(out_addr >> 32)) << 32) |
+                           (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)out_addr);
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(out_u), (short)0, nbytes, 0x00020000);
+    uint8_t* const my_stage = stage + wq * (SPIX * RB);
+    const int sl = lane % LPP;
+    const bool cvalid = n0 + sl * (16 / ESZ) < a.Cout;
 #pragma unroll
-    for (int j = 0; j < MB; ++j) {
-      const int p = wm * (MB * 16) + j * 16 + (lane & 15);
-      const int oy = oy0 + p / TW, ox = ox0 + p % TW;
-      mrow[j] = (p < TH * TW && oy < a.Ho && ox < a.Wo) ? (img * a.Ho + oy) * a.Wo + ox : a.M;
+    for (int r = 0; r < SROUNDS; ++r) {
+      constexpr int RMB = MB / SROUNDS;  // pixel blocks per round
+      static_assert(RMB * SROUNDS == MB, "rounds split the blocks");
+      int mrow[RMB], spix[RMB];
+      v4i ai[NB][RMB];
+      v4f af[NB][RMB];
+#pragma unroll
+      for (int j = 0; j < RMB; ++j) {
+        const int p = wq * (MB * 16) + (r * RMB + j) * 16 + (lane & 15);
+        const int oy = oy0 + p / TW, ox = ox0 + p % TW;
+        mrow[j] = (oy < a.Ho && ox < a.Wo) ? (img * a.Ho + oy) * a.Wo + ox : a.M;
+        spix[j] = j * 16 + (lane & 15);
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+          ai[i][j] = acc_i[i][r * RMB + j];
+          af[i][j] = acc_f[i][r * RMB + j];
+        }
+      }
+      conv_epilogue_rows_staged<KIND, OUT, RMB, NB, RB>(a, ai, af, mrow, n0, 0, ch, my_stage, spix);
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));  // this wavefront's staged rows (LDS ops run in order)
+#pragma unroll
+      for (int c = 0; c < SCH; ++c) {
+        const int pl = c * PPC + lane / LPP;                              // pixel within the round
+        const int p = wq * (MB * 16) + r * SPIX + pl;                     // pixel within the tile
+        typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 v = *reinterpret_cast<const u32x4*>(my_stage + pl * RB + ((sl ^ stage_swz(pl)) & (LPP - 1)) * 16);
+        const int oy = oy0 + p / TW, ox = ox0 + p % TW;
+        const bool ok = cvalid && oy < a.Ho && ox < a.Wo;
+        const uint32_t off =
+            ok ? ((uint32_t)((img * a.Ho + oy) * a.Wo + ox) * (uint32_t)a.out_ld + (uint32_t)n0) * ESZ + sl * 16
+               : OOB;
+        __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, (int)off, 0, 0);
+      }
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));  // the staged rows read before the next round overwrites them
     }
-    // the per-channel operands re-read from LDS for every tile (opaque pointers): kept live across the tile loop, they
-    // would take registers the K loop needs
-    const float *eps = ep_scale, *epb = ep_bias, *epo = ep_osc;
-    asm volatile("" : "+v"(eps), "+v"(epb), "+v"(epo));
-    conv_epilogue_rows<KIND, OUT, MB, NB>(a, acc_i, acc_f, mrow, n0, wn * (NB * 16), eps, epb, epo);
-    if (next < total) {  // the patch loads precede the epilogue's stores, which may stay in flight
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(EPI_STORES));
-      asm volatile("s_barrier" ::: "memory");
+    if (next < total) wait_vm_at_most(SROUNDS * SCH);  // this wavefront's patch loads, issued before its stores
+  };
+
+  for (int ph = 0; ph < n_phases; ++ph) {
+    const int kk = ph - grp;
+    if (kk >= 0) {
+      const int k = kk >> 1;  // the group's k-th tile: the workgroup's tile 2 k + grp
+      const int t = first + (2 * k + grp) * stride;
+      if (k < n_grp) {
+        if ((kk & 1) == 0)
+          k_loop();
+        else
+          epilogue(t, t + 2 * stride);
+      }
     }
+    asm volatile("s_barrier" ::: "memory");
   }
 }
 
-// Patch-tile shapes (TH x TW output pixels, at most 320): the one whose tiles need the fewest per workgroup (the grid
-// holds at most one workgroup per CU), then the least halo. Returns the index into the launch table or -1 when the
-// patch kernel does not apply.
-struct PatchShape { int th, tw; };
-constexpr PatchShape PATCH_SHAPES[] = {{8, 40}, {16, 20}, {10, 32}};
+// Patch tiles: 12 x 16 output pixels x 64 channels.
+constexpr int PATCH_TH = 12, PATCH_TW = 16;
 
 static int64_t patch_grid(int64_t tiles, int64_t n_tiles) {
   // a multiple of 8 (XCDs) and of the channel-block count (each workgroup keeps one), at most one per CU
@@ -1315,49 +1492,27 @@ static int64_t patch_grid(int64_t tiles, int64_t n_tiles) {
   return std::min<int64_t>(cdiv(tiles, unit) * unit, cap);
 }
 
-static int patch_shape(const ConvArgs& a, int lw, bool fast_ok) {
-  if (lw != 16 || !fast_ok || a.x_swz != nullptr || a.pool_out != nullptr || a.a_scale_rows != nullptr) return -1;
-  if (a.Cin != KC || a.kh != 3 || a.kw != 3 || a.sh != 1 || a.sw != 1 || a.dh != 1 || a.dw != 1) return -1;
+// Whether the patch kernel applies: 3 x 3, stride 1, dilation 1, Cin == 128, the fast epilogue's output layout (with a
+// 16-byte aligned output for the whole-line stores), no pooling, per-row scales or pre-swizzled input.
+static bool patch_ok(const ConvArgs& a, int lw, bool fast_ok) {
+  if (lw != 16 || !fast_ok || a.x_swz != nullptr || a.pool_out != nullptr || a.a_scale_rows != nullptr) return false;
+  if (a.Cin != KC || a.kh != 3 || a.kw != 3 || a.sh != 1 || a.sw != 1 || a.dh != 1 || a.dw != 1) return false;
+  if (((uintptr_t)a.out & 15) != 0 || a.out_ld != a.Cout) return false;
   if ((int64_t)a.B * a.H * a.W * a.Cin >= (1LL << 31) - 16 || (int64_t)a.Cout * a.kh * a.kw * a.Cin >= (1LL << 31))
-    return -1;
-  const int64_t n_tiles = cdiv(a.Cout, 64);
-  int best = -1;
-  int64_t best_cost = 0, best_halo = 0;
-  for (int i = 0; i < (int)(sizeof(PATCH_SHAPES) / sizeof(PATCH_SHAPES[0])); ++i) {
-    const PatchShape sh = PATCH_SHAPES[i];
-    const int64_t tiles = (int64_t)a.B * cdiv(a.Ho, sh.th) * cdiv(a.Wo, sh.tw) * n_tiles;
-    if (tiles >= (1LL << 30)) continue;
-    const int64_t cost = cdiv(tiles, patch_grid(tiles, n_tiles)) * sh.th * sh.tw;  // tiles per workgroup x pixels
-    const int64_t halo = (int64_t)(sh.th + 2) * (sh.tw + 2);
-    if (best < 0 || cost < best_cost || (cost == best_cost && halo < best_halo)) {
-      best = i;
-      best_cost = cost;
-      best_halo = halo;
-    }
-  }
-  return best;
-}
-
-template <int KIND, int OUT>
-static void launch_patch_out(const ConvArgs& a, int shape, dim3 grid, hipStream_t stream) {
-  switch (shape) {
-    case 0: conv_patch_kernel<KIND, OUT, 8, 40><<<grid, dim3(512), 0, stream>>>(a); break;
-    case 1: conv_patch_kernel<KIND, OUT, 16, 20><<<grid, dim3(512), 0, stream>>>(a); break;
-    default: conv_patch_kernel<KIND, OUT, 10, 32><<<grid, dim3(512), 0, stream>>>(a); break;
-  }
+    return false;
+  return (int64_t)a.B * cdiv(a.Ho, PATCH_TH) * cdiv(a.Wo, PATCH_TW) * cdiv(a.Cout, 64) < (1LL << 30);
 }
 
 template <int KIND>
-static int launch_patch(ConvArgs a, int shape, hipStream_t stream) {
-  const PatchShape sh = PATCH_SHAPES[shape];
+static int launch_patch(ConvArgs a, hipStream_t stream) {
   a.n_tiles = (int)cdiv(a.Cout, 64);
-  const int64_t tiles = (int64_t)a.B * cdiv(a.Ho, sh.th) * cdiv(a.Wo, sh.tw) * a.n_tiles;
+  const int64_t tiles = (int64_t)a.B * cdiv(a.Ho, PATCH_TH) * cdiv(a.Wo, PATCH_TW) * a.n_tiles;
   const dim3 grid((unsigned)patch_grid(tiles, a.n_tiles));
   constexpr int QOUT = KIND == KIND_INT8 ? OUT_INT8 : OUT_E4M3;
   if (a.out_mode == OUT_BF16)
-    launch_patch_out<KIND, OUT_BF16>(a, shape, grid, stream);
+    conv_patch_kernel<KIND, OUT_BF16, PATCH_TH, PATCH_TW><<<grid, dim3(512), 0, stream>>>(a);
   else
-    launch_patch_out<KIND, QOUT>(a, shape, grid, stream);
+    conv_patch_kernel<KIND, QOUT, PATCH_TH, PATCH_TW><<<grid, dim3(512), 0, stream>>>(a);
   return launch_status();
 }
 
@@ -1483,7 +1638,7 @@ static int launch_conv(ConvArgs a, hipStream_t stream) {
   a.m_tiles = (int)m_tiles;
   a.m_base = 0;
   const bool fast_ok = a.out_mode == OUT_BF16 ? conv_fast_ok<OUT_BF16>(a) : conv_fast_ok<OUT_INT8>(a);
-  if (const int shape = patch_shape(a, lw, fast_ok); shape >= 0) return launch_patch<KIND>(a, shape, stream);
+  if (patch_ok(a, lw, fast_ok)) return launch_patch<KIND>(a, stream);
   if (const int wm = wide_wm(a, lw)) {
     a.n_tiles = (int)cdiv((int64_t)a.Cout, (8 / wm) * 64);
     a.m_tiles = (int)cdiv((int64_t)a.M, wm * 80);
