@@ -1516,6 +1516,277 @@ static int launch_patch(ConvArgs a, hipStream_t stream) {
   return launch_status();
 }
 
+// ---- Pointwise, register operands --------------------------------------------------------------------------------
+// Pointwise (1 x 1, stride 1) convolutions, a GEMM over pixels, with Cin % 128 == 0, Cin <= 512 and Cout >= 128, where
+// the epilogue (GELU above all) outweighs the MFMAs. Persistent workgroups of 8 wavefronts, one per CU, keep the
+// weights of 128 output channels in LDS (128 x Cin bytes, read-only after the prologue); every wavefront then works
+// alone, with no barrier: it loads its 32 pixel rows of activations straight into MFMA operand registers (the next
+// tile's rows), runs 2 x 8 blocks of 16 x 16 against the LDS weights, and writes
+// its epilogue through a private LDS staging area in whole lines. Two wavefronts per SIMD drift apart, so one's loads
+// and MFMAs run while the other's epilogue keeps the VALU busy.
+template <int KIND, int OUT, int KS>
+__global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
+  constexpr int BN = 128, MB = 2, NB = 8, TMW = MB * 16;  // a wavefront's tile: 32 pixels x 128 channels
+  constexpr int WTS_BYTES = KS * BN * KC;                // [K step][channel][128 B]
+  constexpr int WEXP_BYTES = KIND == KIND_MX ? BN * KS * 4 : 16;
+  constexpr int ESZ = OUT == OUT_BF16 ? 2 : 1;
+  constexpr int RB = BN * ESZ, LPP = RB / 16, PPC = 64 / LPP;  // staged row: the 128 channels of one pixel
+  constexpr int SCH = 16 / PPC;                                 // 1 KB stores per 16-pixel round
+  static_assert(SCH * PPC == 16, "whole stores per round");
+  constexpr int STAGE_BYTES = 8 * 16 * RB;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[WTS_BYTES + STAGE_BYTES + WEXP_BYTES + 3 * BN * 4 + 16];
+  uint8_t* const wts = smem;
+  uint8_t* const stage = wts + WTS_BYTES;
+  uint8_t* const wexp_s = stage + STAGE_BYTES;           // [channel][K block] (MXFP8)
+  float* const ep_scale = reinterpret_cast<float*>(wexp_s + WEXP_BYTES);
+  float* const ep_bias = ep_scale + BN;
+  float* const ep_osc = ep_bias + BN;
+  uint8_t* const xexp_s = reinterpret_cast<uint8_t*>(ep_osc + BN);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4;
+
+  // tiles: 8 x 32 pixels x 128 channels, wavefront w taking pixels [32 w, +32); XCD-aware deal as in the patch kernel,
+  // the workgroup keeping one channel block
+  const int m_tiles = (a.M + 8 * TMW - 1) / (8 * TMW);
+  const int total = a.n_tiles * m_tiles;
+  const int stride = gridDim.x;
+  const int per_xcd = stride >> 3;
+  const int first = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (first >= total) return;
+  const int n0 = (first % a.n_tiles) * BN;
+
+  const int x_nrec = __builtin_amdgcn_readfirstlane((int)((int64_t)a.M * a.Cin));
+  const int w_nrec = __builtin_amdgcn_readfirstlane(a.Cout * a.Cin);
+  constexpr uint32_t OOB = 0x80000000u;
+#pragma unroll
+  for (int i = 0; i < KS * BN / 64; ++i) {  // weights: chunk k (8 channels x 128 bytes of one K step) = wave + 8 i
+    const int k = wave + 8 * i;
+    const int ks = k / (BN / 8), r = 8 * (k % (BN / 8)) + (lane >> 3);
+    const int seg = (lane & 7) ^ patch_swz(r);
+    const uint32_t off = n0 + r < a.Cout ? (uint32_t)((n0 + r) * a.Cin + ks * KC + seg * 16) : OOB;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), (short)0, w_nrec, 0x00020000),
+        (lds_void_t*)(wts + k * 1024), 16, off, 0, 0, 0);
+  }
+  if (tid < BN) {
+    const int n = n0 + tid;
+    const bool nok = n < a.Cout;
+    ep_scale[tid] = (KIND == KIND_INT8 && nok) ? *a.a_scale * a.w_scale[n] : 1.0f;
+    float bias = -0.0f;
+    if (a.bias != nullptr && nok)
+      bias = a.bias_dtype == FIM_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(a.bias)[n])
+                                      : static_cast<const float*>(a.bias)[n];
+    ep_bias[tid] = bias;
+    ep_osc[tid] = (OUT == OUT_E4M3 && nok) ? exp2_int((int)a.out_expo[n >> 5]) : 1.0f;
+  }
+  if constexpr (KIND == KIND_MX) {
+    constexpr int WEXP_N = BN * KS * 4, WEXP_PASSES = (WEXP_N + 511) / 512;
+    const int64_t wexp_valid = ((int64_t)a.Cout - n0) * (KS * 4);
+    int e[WEXP_PASSES];
+#pragma unroll
+    for (int i = 0; i < WEXP_PASSES; ++i) {
+      const int idx = tid + 512 * i;
+      e[i] = idx < WEXP_N && idx < wexp_valid ? (int)a.w_expo[(int64_t)n0 * (KS * 4) + idx] + 127 : 127;
+    }
+#pragma unroll
+    for (int i = 0; i < WEXP_PASSES; ++i)
+      if (tid + 512 * i < WEXP_N) wexp_s[tid + 512 * i] = (uint8_t)e[i];
+    if (tid < KS * 4) xexp_s[tid] = (uint8_t)((int)a.x_expo[tid] + 127);
+  }
+
+  // activation operands straight from global memory: block j, K step ks is the lane's row's bytes [16 g, +16) and
+  // [64 + 16 g, +16) of the step (rows past M read as zero)
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.x), (short)0, x_nrec, 0x00020000);
+  auto load_x = [&](int t, v8i (&xa)[MB][KS]) __attribute__((always_inline)) {
+    const int m0 = (t / a.n_tiles) * (8 * TMW) + wave * TMW;
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const int m = m0 + j * 16 + (lane & 15);
+      const uint32_t base = m < a.M ? (uint32_t)(m * a.Cin + 16 * g) : OOB;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const v4i lo = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)(base + ks * KC), 0, 0));
+        const v4i hi =
+            __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)(base + ks * KC + 64), 0, 0));
+        xa[j][ks] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+    }
+  };
+
+  int wo[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int r = i * 16 + (lane & 15);
+    wo[i] = r * KC + ((g ^ patch_swz(r)) << 4);
+  }
+  auto read_w = [&](int ofs) __attribute__((always_inline)) {
+    const v4i lo = *reinterpret_cast<const v4i*>(smem + ofs);
+    const v4i hi = *reinterpret_cast<const v4i*>(smem + (ofs ^ 64));
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+
+  int sxs[KS], swp[KS][2];
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+  asm volatile("s_barrier" ::: "memory");  // the weights and staged operands (the last barrier of the kernel)
+  if constexpr (KIND == KIND_MX) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      sxs[ks] = xexp_s[ks * 4 + g];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          packed |= (uint32_t)wexp_s[((4 * h + i) * 16 + (lane & 15)) * (KS * 4) + ks * 4 + g] << (8 * i);
+        swp[ks][h] = (int)packed;
+      }
+    }
+  }
+
+  const int nbytes = __builtin_amdgcn_readfirstlane((int)((uint32_t)a.M * (uint32_t)a.out_ld * ESZ));
+  const uint64_t out_addr = (uint64_t)a.out;
+  const uint64_t out_u = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(out_addr >> 32)) << 32) |
+                         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)out_addr);
+  const __amdgpu_buffer_rsrc_t orsrc =
+      __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(out_u), (short)0, nbytes, 0x00020000);
+  uint8_t* const my_stage = stage + wave * (16 * RB);
+
+  // one tile: its operand loads are waited for right away; the other wavefront on the SIMD runs meanwhile
+  auto run_tile = [&](int t) __attribute__((always_inline)) {
+    v8i xc[MB][KS];
+    load_x(t, xc);
+    int wq[NB];  // weight offsets made opaque per tile (else all K steps' weight operands are hoisted)
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      wq[i] = wo[i];
+      asm volatile("" : "+v"(wq[i]));
+    }
+    v4i acc_i[NB][MB];
+    v4f acc_f[NB][MB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int j = 0; j < MB; ++j) {
+        acc_i[i][j] = v4i{0, 0, 0, 0};
+        acc_f[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+      }
+    v8i wc[2];
+    wc[0] = read_w(wq[0]);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const int nx = ks * NB + i + 1;  // the next weight block, read while this one's MFMAs run
+        if (nx < KS * NB) wc[nx & 1] = read_w(wq[nx % NB] + (nx / NB) * (BN * KC));
+        const v8i& w = wc[(ks * NB + i) & 1];
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+          if constexpr (KIND == KIND_INT8) {
+            acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_shufflevector(w, w, 0, 1, 2, 3),
+                                                                __builtin_shufflevector(xc[j][ks], xc[j][ks], 0, 1, 2, 3),
+                                                                acc_i[i][j], 0, 0, 0);
+            acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_shufflevector(w, w, 4, 5, 6, 7),
+                                                                __builtin_shufflevector(xc[j][ks], xc[j][ks], 4, 5, 6, 7),
+                                                                acc_i[i][j], 0, 0, 0);
+          } else {
+            acc_f[i][j] = mfma_scale_opsel(w, xc[j][ks], acc_f[i][j], i & 3, swp[ks][i >> 2], sxs[ks]);
+          }
+        }
+      }
+    // the accumulators pinned (else the MFMAs are sunk into the epilogue with their operands live)
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int j = 0; j < MB; ++j) {
+        if constexpr (KIND == KIND_INT8)
+          asm volatile("" : "+v"(acc_i[i][j]));
+        else
+          asm volatile("" : "+v"(acc_f[i][j]));
+      }
+    // epilogue: 16 pixels per round, staged in this wavefront's LDS area and written in whole lines
+    const int m0 = (t / a.n_tiles) * (8 * TMW) + wave * TMW;
+    const int sl = lane % LPP;
+    const bool cvalid = n0 + sl * (16 / ESZ) < a.Cout;
+#pragma unroll
+    for (int r = 0; r < MB; ++r) {
+      int mrow[1], spix[1];
+      const int m = m0 + r * 16 + (lane & 15);
+      mrow[0] = m < a.M ? m : a.M;
+      spix[0] = lane & 15;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {  // channel halves: 4 blocks' per-channel operands in registers at a time
+        int eo = 0;
+        asm volatile("" : "+v"(eo));
+        const EpiChannels<4> ch = epi_channels<4>(64 * h, ep_scale + eo, ep_bias + eo, ep_osc + eo);
+        v4i ai[4][1];
+        v4f af[4][1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ai[i][0] = acc_i[4 * h + i][r];
+          af[i][0] = acc_f[4 * h + i][r];
+        }
+        conv_epilogue_rows_staged<KIND, OUT, 1, 4, RB>(a, ai, af, mrow, n0, 64 * h, ch, my_stage, spix);
+      }
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
+#pragma unroll
+      for (int c = 0; c < SCH; ++c) {
+        const int pl = c * PPC + lane / LPP;
+        typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 v = *reinterpret_cast<const u32x4*>(my_stage + pl * RB + ((sl ^ stage_swz(pl)) & (LPP - 1)) * 16);
+        const int mm = m0 + r * 16 + pl;
+        const uint32_t off = cvalid && mm < a.M ? ((uint32_t)mm * (uint32_t)a.out_ld + (uint32_t)n0) * ESZ + sl * 16
+                                                : OOB;
+        __builtin_amdgcn_raw_buffer_store_b128(v, orsrc, (int)off, 0, 0);
+      }
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
+    }
+  };
+
+  for (int t = first; t < total; t += stride) run_tile(t);
+}
+
+// Whether the pointwise kernel applies: 1 x 1, stride 1, no padding, 128 <= Cin <= 512 with Cin % 128 == 0,
+// Cout >= 128 (Cout % 16 == 0 by the fast epilogue), dense 16-byte aligned output, no pooling / per-row scales.
+static int pw_ks(const ConvArgs& a, int lw, bool fast_ok) {
+  if (lw != 16 || !fast_ok || a.x_swz != nullptr || a.pool_out != nullptr || a.a_scale_rows != nullptr) return 0;
+  if (a.kh != 1 || a.kw != 1 || a.sh != 1 || a.sw != 1 || a.ph != 0 || a.pw != 0) return 0;
+  if (a.Cin % KC != 0 || a.Cin > 4 * KC || a.Cout < 128 || ((uintptr_t)a.out & 15) != 0 || a.out_ld != a.Cout)
+    return 0;
+  if ((int64_t)a.M * a.Cin >= (1LL << 31) - 16 || (int64_t)a.Cout * a.Cin >= (1LL << 31)) return 0;
+  // at least two 256-pixel tiles per CU: with fewer, most wavefronts run one tile with nothing to overlap its loads
+  // and epilogue against, and the one-round wide tiles are faster (config 2: 19.4 against 25 us; the refiner
+  // stack's many-round layers: 19.0 -> 18.1 ms)
+  if (cdiv((int64_t)a.M, 256) * cdiv((int64_t)a.Cout, 128) < 2 * device_cus()) return 0;
+  return a.Cin / KC;
+}
+
+template <int KIND, int OUT>
+static void launch_pw_out(const ConvArgs& a, int ks, dim3 grid, hipStream_t stream) {
+  switch (ks) {
+    case 1: conv_pw_kernel<KIND, OUT, 1><<<grid, dim3(512), 0, stream>>>(a); break;
+    case 2: conv_pw_kernel<KIND, OUT, 2><<<grid, dim3(512), 0, stream>>>(a); break;
+    case 3: conv_pw_kernel<KIND, OUT, 3><<<grid, dim3(512), 0, stream>>>(a); break;
+    default: conv_pw_kernel<KIND, OUT, 4><<<grid, dim3(512), 0, stream>>>(a); break;
+  }
+}
+
+template <int KIND>
+static int launch_pw(ConvArgs a, int ks, hipStream_t stream) {
+  a.n_tiles = (int)cdiv(a.Cout, 128);
+  const int64_t tiles = cdiv((int64_t)a.M, 256) * a.n_tiles;
+  const dim3 grid((unsigned)patch_grid(tiles, a.n_tiles));
+  constexpr int QOUT = KIND == KIND_INT8 ? OUT_INT8 : OUT_E4M3;
+  if (a.out_mode == OUT_BF16)
+    launch_pw_out<KIND, OUT_BF16>(a, ks, grid, stream);
+  else
+    launch_pw_out<KIND, QOUT>(a, ks, grid, stream);
+  return launch_status();
+}
+
 template <int KIND, int WM>
 static void launch_wide(const ConvArgs& a, dim3 grid, hipStream_t stream) {
   constexpr int QOUT = KIND == KIND_INT8 ? OUT_INT8 : OUT_E4M3;
@@ -1639,6 +1910,7 @@ static int launch_conv(ConvArgs a, hipStream_t stream) {
   a.m_base = 0;
   const bool fast_ok = a.out_mode == OUT_BF16 ? conv_fast_ok<OUT_BF16>(a) : conv_fast_ok<OUT_INT8>(a);
   if (patch_ok(a, lw, fast_ok)) return launch_patch<KIND>(a, stream);
+  if (const int ks = pw_ks(a, lw, fast_ok)) return launch_pw<KIND>(a, ks, stream);
   if (const int wm = wide_wm(a, lw)) {
     a.n_tiles = (int)cdiv((int64_t)a.Cout, (8 / wm) * 64);
     a.m_tiles = (int)cdiv((int64_t)a.M, wm * 80);

@@ -471,3 +471,68 @@ def test_mxfp8_conv2d_patch_tiles(case):
         got_q = hip(*args, *geo, out_exponent=oe.to(DEV))
         assert torch.equal(got_q.view(torch.uint8), ops.quantize_mxfp8(hip(*args, *geo), oe.to(DEV)).values
                            .view(torch.uint8)), name
+
+
+# (name, image (B, H, W), Cin, Cout): pointwise shapes (1 x 1, stride 1, Cin a multiple of 128 up to 512, Cout >= 128):
+# 1 to 4 K steps, a partial last tile of pixels, a partial channel block; the large ones run the register-operand
+# pointwise kernel, the small ones the one-round kernels
+ROW_CASES = [
+    ("k1_partial_tile", (1, 7, 13), 128, 128),
+    ("k2_n144", (2, 9, 11), 256, 144),
+    ("k3_n256", (1, 30, 31), 384, 256),
+    ("k4_n512_many", (2, 60, 70), 512, 512),
+    # at least two 256-pixel tiles per CU (the kernel's condition on 256 CUs)
+    ("k1_n128_big", (2, 256, 257), 128, 128),
+    ("k2_n144_big", (1, 256, 257), 256, 144),
+    ("k3_n256_big", (2, 160, 210), 384, 256),
+    ("k4_n512_big", (2, 128, 129), 512, 512),
+]
+PW_GEO = (1, 1, 1, 1, 0, 0, 1, 1)
+
+
+@pytest.mark.parametrize("case", range(len(ROW_CASES)))
+def test_int8_conv2d_pointwise_tiles(case):
+    """INT8 through the pointwise kernel: bit-exact BF16 out (bias + ReLU), with a dense residual, and INT8 out."""
+    name, shape, cin, cout = ROW_CASES[case]
+    x, weight, a_scale, w_scale, bias = _int8_inputs(cin, cout, 1, 1, True, shape=shape)
+    args = _dev(x, weight, a_scale, w_scale, bias)
+    hip = ops.int8_conv2d.get("hip")
+    got = hip(*args, *PW_GEO, relu=True).cpu()
+    want = ref.int8_conv2d(x, weight, a_scale, w_scale, bias, *PW_GEO, relu=True)
+    assert torch.equal(got, want), name
+    res = (torch.randn(*want.shape) * 4).to(torch.bfloat16)
+    got_r = hip(*args, *PW_GEO, relu=True, residual=res.to(DEV)).cpu()
+    assert torch.equal(got_r, ref.int8_conv2d(x, weight, a_scale, w_scale, bias, *PW_GEO, relu=True, residual=res)), name
+    out_scale = torch.tensor(0.09)
+    got_q = hip(*args, *PW_GEO, out_scale=out_scale.to(DEV)).cpu()
+    assert torch.equal(got_q, ref.int8_conv2d(x, weight, a_scale, w_scale, bias, *PW_GEO, out_scale=out_scale)), name
+
+
+@pytest.mark.parametrize("case", range(len(ROW_CASES)))
+def test_mxfp8_conv2d_pointwise_tiles(case):
+    """MXFP8 through the pointwise kernel: the oracle bar (plain; GELU; GELU with a residual), and the E4M3 output
+    byte-identical to quantizing the kernel's own BF16 output."""
+    name, shape, cin, cout = ROW_CASES[case]
+    torch.manual_seed(100 + case)
+    x = (torch.randn(*shape, cin) * 3).to(torch.float8_e4m3fn)
+    ce = torch.randint(-6, 3, (cin // 32,), dtype=torch.int8)
+    w = (torch.randn(cout, cin) * 2).to(torch.float8_e4m3fn)
+    we = torch.randint(-10, -4, (cout, cin // 32), dtype=torch.int8)
+    bias = torch.randn(cout).to(torch.bfloat16)
+    hip = ops.mxfp8_conv2d.get("hip")
+    args = _dev(x, ce, w, we, bias)
+    got = hip(*args, *PW_GEO).cpu()
+    want = ref.mxfp8_conv2d(x, ce, w, we, bias, *PW_GEO)
+    _assert_mx_close(got, want)
+    got_g = hip(*args, *PW_GEO, gelu=True).cpu().float()
+    want_g = ref.mxfp8_conv2d(x, ce, w, we, bias, *PW_GEO, gelu=True).float()
+    assert (got_g - want_g).norm() / want_g.norm() <= 1e-3, name
+    res = (torch.randn(*want.shape) * 2).to(torch.bfloat16)
+    got_r = hip(*args, *PW_GEO, gelu=True, residual=res.to(DEV)).cpu().float()
+    want_r = ref.mxfp8_conv2d(x, ce, w, we, bias, *PW_GEO, gelu=True, residual=res).float()
+    assert (got_r - want_r).norm() / want_r.norm() <= 1e-3, name
+    if cout % 32 == 0:
+        oe = torch.full((cout // 32,), -1, dtype=torch.int8)
+        got_q = hip(*args, *PW_GEO, out_exponent=oe.to(DEV))
+        assert torch.equal(got_q.view(torch.uint8), ops.quantize_mxfp8(hip(*args, *PW_GEO), oe.to(DEV)).values
+                           .view(torch.uint8)), name
