@@ -219,7 +219,6 @@ def dwpw_block():
     return {
         "mxfp8_fused": lambda: ops.depthwise5x5_relu_pointwise_mxfp8(*mx),
         "mxfp8_composite": lambda: hip_conv.pointwise_mxfp8_composite(*mx),
-        "int8_fused": lambda: hip_conv.pointwise_int8_fused(*i8),
         "int8_op": lambda: ops.depthwise5x5_relu_pointwise_int8(*i8),
         "int8_composite": lambda: hip_conv.pointwise_int8_composite(*i8),
     }, {"bytes": nbytes}

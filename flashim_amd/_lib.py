@@ -59,8 +59,6 @@ SIGNATURES: dict[str, list] = {
     "fim_depthwise5x5": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp],
     "fim_depthwise5x5_relu_pointwise_mxfp8": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _vp,
                                               _vp],
-    "fim_depthwise5x5_relu_pointwise_int8": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i32,
-                                             _vp, _vp],
     "fim_test_e4m3": [_vp, _i64, _vp, _vp],
     "fim_test_mx_exponent": [_vp, _i64, _vp, _vp],
     "fim_test_bf16": [_vp, _i64, _vp, _vp],

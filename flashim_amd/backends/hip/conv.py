@@ -10,8 +10,7 @@
 * ``depthwise5x5_relu_pointwise_mxfp8`` (``flashim/ops/conv.py:93-113``) -> at C = 128 with a 128 x 128 pointwise
   weight ``fim_depthwise5x5_relu_pointwise_mxfp8`` (one kernel, the reference's fused shapes
   ``flashim/backends/triton/conv.py:310-508``), else the producer then ``fim_mxfp8_scaled_mm``
-* ``depthwise5x5_relu_pointwise_int8`` (``flashim/ops/conv.py:119-138``) -> the producer then ``fim_int8_linear`` (the
-  measured faster of the two; ``fim_depthwise5x5_relu_pointwise_int8`` is ``pointwise_int8_fused``, same bits)
+* ``depthwise5x5_relu_pointwise_int8`` (``flashim/ops/conv.py:119-138``) -> the producer then ``fim_int8_linear``
 
 ``gelu=`` on the two convs is an epilogue FlashIM's conv ops do not have: it is ``int8_linear``'s GELU
 (``flashim/ops/gemm.py:94-95``): ``F.gelu`` of the BF16 result, rounded to BF16, before the residual.
@@ -202,22 +201,8 @@ def depthwise5x5_relu_pointwise_int8(value: Tensor, dw_weight: Tensor, dw_bias: 
                                      pw_wscale: Tensor, pw_bias: Tensor, scale: Tensor) -> Tensor:
     """The INT8 refiner block (``flashim/ops/conv.py:119-138``) -> ``[B, C, H, W]`` view of NHWC BF16: the two-launch
     composite at every shape. Its INT8 intermediate is 1 byte per element, and on MI355X at 2 x 128 x 400 x 400 the
-    composite measures 84 us against 90 us for the one-kernel ``pointwise_int8_fused``, which gives the same bits."""
+    composite measured 84 us against 90 us for a one-kernel version, which gave the same bits."""
     return pointwise_int8_composite(value, dw_weight, dw_bias, pw_weight, pw_wscale, pw_bias, scale)
-
-
-def pointwise_int8_fused(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor, pw_wscale: Tensor,
-                         pw_bias: Tensor, scale: Tensor) -> Tensor:
-    """One kernel (``fim_depthwise5x5_relu_pointwise_int8``) at C = 128 with a 128 x 128 pointwise weight; bit for bit
-    the composite."""
-    if not _fused_pointwise_shape(value, pw_weight):
-        raise ValueError(f"pointwise_int8_fused needs C = 128 and a 128 x 128 weight, got {tuple(value.shape)}, "
-                         f"{tuple(pw_weight.shape)}")
-    x, dw_w, dw_b = _dw_operands(value, dw_weight, dw_bias)
-    out = library.depthwise5x5_relu_pointwise_int8(
-        x, dw_w, dw_b, pw_weight.contiguous(), pw_wscale.to(device=value.device, dtype=torch.float32).reshape(-1)
-        .contiguous(), _scalar(scale, value.device), _bias(pw_bias, value.device))
-    return out.permute(0, 3, 1, 2)
 
 
 def pointwise_int8_composite(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,

@@ -1,12 +1,10 @@
-// Depthwise 5x5 + bias + ReLU -> quantize -> pointwise GEMM + bias in one kernel, the two fused refiner blocks of
-// flashim/backends/triton/conv.py:310-508 (ops flashim/ops/conv.py:93-138):
-//   MXFP8  depthwise5x5_relu_pointwise_mxfp8: relu(dwconv + bias) in FP32 -> dynamic per-(pixel, 32-channel) MXFP8
-//          -> block-scaled GEMM with the weight's E8M0 bytes (+ bias) -> BF16
-//   INT8   depthwise5x5_relu_pointwise_int8: relu(dwconv + bias) -> BF16 -> static INT8 -> int8_linear
-//          (acc * (a_scale * w_scale[n]) + bias) -> BF16
-// for C = 128 input channels and a 128 x 128 pointwise weight (the reference's fused shapes). The quantized activations
-// never leave the CU: the result is, bit for bit, the two-launch composite (depthwise producer, then
-// fim_mxfp8_scaled_mm / fim_int8_linear) with the same MFMA per 16 x 16 output block.
+// Depthwise 5x5 + bias + ReLU -> quantize -> pointwise GEMM + bias in one kernel, the fused MXFP8 refiner block of
+// flashim/backends/triton/conv.py:310-420 (op flashim/ops/conv.py:93-117, depthwise5x5_relu_pointwise_mxfp8):
+// relu(dwconv + bias) in FP32 -> dynamic per-(pixel, 32-channel) MXFP8 -> block-scaled GEMM with the weight's E8M0
+// bytes (+ bias) -> BF16, for C = 128 input channels and a 128 x 128 pointwise weight (the reference's fused shape).
+// The quantized activations never leave the CU: the result is, bit for bit, the two-launch composite (depthwise
+// producer, then fim_mxfp8_scaled_mm) with the same MFMA per 16 x 16 output block. (The INT8 block runs as that
+// two-launch composite: its intermediate is 1 byte per element, and the composite measured faster than a fused kernel.)
 //
 // Tile: 32 columns x 8 rows of one image, all 128 channels, per 256-lane workgroup (2 per CU by LDS):
 //   depthwise, per 32-channel slice: the 12 x 36-pixel input window is staged channel-planar in LDS and the taps run
@@ -28,16 +26,13 @@ constexpr int DP_OROW = DP_TW * DP_CS + 16;           // dwords per staged FP32 
 constexpr int DP_STAGE = DP_CS * DP_PLANE;            // 6976 dwords
 static_assert(4 * DP_OROW <= DP_STAGE, "a 4-row output half fits in the input window's space");
 
-enum { DP_MX = 0, DP_INT8 = 1 };
 
 struct DwPwArgs {
   const uint16_t* x;        // BF16 [B, H, W, 128]
   const uint16_t* dw_w;     // BF16 [25, 128]
   const float* dw_b;        // FP32 [128]
-  const uint8_t* pw_w;      // E4M3 / INT8 [128, 128]
-  const uint8_t* pw_e8m0;   // MX: [128, 4] E8M0 bytes
-  const float* pw_wscale;   // INT8: [128]
-  const float* a_scale;     // INT8: the static activation scale
+  const uint8_t* pw_w;      // E4M3 [128, 128]
+  const uint8_t* pw_e8m0;   // [128, 4] E8M0 bytes
   const void* pw_b;         // [128] or null
   int pw_b_dtype;
   uint16_t* out;            // BF16 [B, H, W, 128]
@@ -48,13 +43,12 @@ struct DwPwArgs {
 
 typedef __bf16 v4bf16 __attribute__((ext_vector_type(4)));
 
-template <int KIND>
 __global__ __launch_bounds__(256, 2) void dw_pw_kernel(const DwPwArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t sm[DP_STAGE];           // input window / FP32 output half
   __shared__ __attribute__((aligned(16))) uint8_t act[DP_PX * DP_C];       // quantized activations [px][128 B]
   __shared__ __attribute__((aligned(16))) uint8_t wts[DP_N * DP_C];        // pointwise weight [n][128 B]
   __shared__ int8_t aexp[DP_PX * 4];                                        // MX exponents [px][32-channel block]
-  __shared__ float pb[DP_N], ps[DP_N];                                      // pointwise bias, INT8 output scale
+  __shared__ float pb[DP_N];                                                // pointwise bias
   __shared__ uint8_t pe[DP_N * 4];                                          // MX weight E8M0 [n][block]
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -80,13 +74,7 @@ __global__ __launch_bounds__(256, 2) void dw_pw_kernel(const DwPwArgs a) {
       bias = a.pw_b_dtype == FIM_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(a.pw_b)[tid])
                                       : static_cast<const float*>(a.pw_b)[tid];
     pb[tid] = bias;
-    ps[tid] = KIND == DP_INT8 ? *a.a_scale * a.pw_wscale[tid] : 1.0f;
-    if (KIND == DP_MX) *reinterpret_cast<uint32_t*>(&pe[4 * tid]) = reinterpret_cast<const uint32_t*>(a.pw_e8m0)[tid];
-  }
-  float oscale = 1.0f, oinv = 1.0f;
-  if (KIND == DP_INT8) {
-    oscale = *a.a_scale;
-    oinv = __fdiv_rn(1.0f, oscale);
+    *reinterpret_cast<uint32_t*>(&pe[4 * tid]) = reinterpret_cast<const uint32_t*>(a.pw_e8m0)[tid];
   }
 
   // ---- depthwise, one 32-channel slice at a time -------------------------------------------------------------------
@@ -184,32 +172,18 @@ __global__ __launch_bounds__(256, 2) void dw_pw_kernel(const DwPwArgs a) {
         float v[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
         uint2 codes;
         const int p = (4 * half + rl) * DP_TW + col;  // tile pixel
-        if (KIND == DP_MX) {
-          float amax = 0.f;
+        float amax = 0.f;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
-          amax = fmaxf(amax, __shfl_xor(amax, 1));
-          amax = fmaxf(amax, __shfl_xor(amax, 2));
-          const int ex = mx_exponent_from_amax(amax);
-          const float inv = exp2_int(-ex);
-          codes = make_uint2(pack_e4m3x4(mx_scale_clamp(v[0], inv), mx_scale_clamp(v[1], inv),
-                                         mx_scale_clamp(v[2], inv), mx_scale_clamp(v[3], inv)),
-                             pack_e4m3x4(mx_scale_clamp(v[4], inv), mx_scale_clamp(v[5], inv),
-                                         mx_scale_clamp(v[6], inv), mx_scale_clamp(v[7], inv)));
-          if (part == 0) aexp[p * 4 + s] = (int8_t)ex;
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; e += 2) round_bf16x2(v[e], v[e + 1]);
-          int qi[8];
-          quantize_int8_fast_n<8>(v, oscale, oinv, qi);
-          uint32_t q0 = 0, q1 = 0;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            q0 |= (uint32_t)(uint8_t)qi[e] << (8 * e);
-            q1 |= (uint32_t)(uint8_t)qi[4 + e] << (8 * e);
-          }
-          codes = make_uint2(q0, q1);
-        }
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+        amax = fmaxf(amax, __shfl_xor(amax, 1));
+        amax = fmaxf(amax, __shfl_xor(amax, 2));
+        const int ex = mx_exponent_from_amax(amax);
+        const float inv = exp2_int(-ex);
+        codes = make_uint2(pack_e4m3x4(mx_scale_clamp(v[0], inv), mx_scale_clamp(v[1], inv),
+                                       mx_scale_clamp(v[2], inv), mx_scale_clamp(v[3], inv)),
+                           pack_e4m3x4(mx_scale_clamp(v[4], inv), mx_scale_clamp(v[5], inv),
+                                       mx_scale_clamp(v[6], inv), mx_scale_clamp(v[7], inv)));
+        if (part == 0) aexp[p * 4 + s] = (int8_t)ex;
         const int seg = 2 * s + (part >> 1);  // 16-byte slot of channels [32 s + 8 part, + 8)
         *reinterpret_cast<uint2*>(&act[p * DP_C + ((seg ^ ((p >> 1) & 7)) << 4) + 8 * (part & 1)]) = codes;
       }
@@ -220,25 +194,18 @@ __global__ __launch_bounds__(256, 2) void dw_pw_kernel(const DwPwArgs a) {
   // ---- pointwise: wave w, pixels [64 w, 64 w + 64), output channels in two passes of 64 --------------------------
   const int g = lane >> 4, r16 = lane & 15;
   v8i xf[4];
-  v4i xlo[4], xhi[4];
   int sx[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int p = 64 * wave + 16 * j + r16;
     const v4i lo = *reinterpret_cast<const v4i*>(&act[p * DP_C + ((g ^ ((p >> 1) & 7)) << 4)]);
     const v4i hi = *reinterpret_cast<const v4i*>(&act[p * DP_C + (((g + 4) ^ ((p >> 1) & 7)) << 4)]);
-    if (KIND == DP_MX) {
-      xf[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      sx[j] = (int)aexp[p * 4 + g] + 127;  // lane group g scales K block g = channel slice g
-    } else {
-      xlo[j] = lo;
-      xhi[j] = hi;
-    }
+    xf[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    sx[j] = (int)aexp[p * 4 + g] + 127;  // lane group g scales K block g = channel slice g
   }
 #pragma unroll
   for (int pass = 0; pass < 2; ++pass) {
     v4f acc_f[4][4];
-    v4i acc_i[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int n = 64 * pass + 16 * i + r16;
@@ -246,17 +213,12 @@ __global__ __launch_bounds__(256, 2) void dw_pw_kernel(const DwPwArgs a) {
       const v4i wh = *reinterpret_cast<const v4i*>(&wts[n * DP_C + (((g + 4) ^ ((n >> 1) & 7)) << 4)]);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        if (KIND == DP_MX) {
-          const v8i wf = __builtin_shufflevector(wl, wh, 0, 1, 2, 3, 4, 5, 6, 7);
-          acc_f[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf, xf[j], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0,
-                                                                         (int)pe[n * 4 + g], 0, sx[j]);
-        } else {
-          acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl, xlo[j], v4i{0, 0, 0, 0}, 0, 0, 0);
-          acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh, xhi[j], acc_i[i][j], 0, 0, 0);
-        }
+        const v8i wf = __builtin_shufflevector(wl, wh, 0, 1, 2, 3, 4, 5, 6, 7);
+        acc_f[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf, xf[j], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0,
+                                                                       (int)pe[n * 4 + g], 0, sx[j]);
       }
     }
-    // epilogue: + bias (INT8: acc * (a_scale * w_scale[n]) first), BF16, 4 channels of one pixel per store
+    // epilogue: + bias, BF16, 4 channels of one pixel per store
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int p = 64 * wave + 16 * j + r16;
@@ -269,8 +231,7 @@ __global__ __launch_bounds__(256, 2) void dw_pw_kernel(const DwPwArgs a) {
         float yv[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const float t = KIND == DP_MX ? acc_f[i][j][v] : __fmul_rn((float)acc_i[i][j][v], ps[n0 + v]);
-          yv[v] = __fadd_rn(t, pb[n0 + v]);
+          yv[v] = __fadd_rn(acc_f[i][j][v], pb[n0 + v]);
         }
         if (ok) *reinterpret_cast<uint2*>(dst + n0) = make_uint2(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]));
       }
@@ -282,7 +243,7 @@ __global__ __launch_bounds__(256, 2) void dw_pw_kernel(const DwPwArgs a) {
 
 using namespace fim;
 
-static int dwpw_launch(const DwPwArgs& a, int kind, int64_t C, int64_t N, hipStream_t stream) {
+static int dwpw_launch(const DwPwArgs& a, int64_t C, int64_t N, hipStream_t stream) {
   if (a.x == nullptr || a.dw_w == nullptr || a.dw_b == nullptr || a.pw_w == nullptr || a.out == nullptr)
     return FIM_ERR_INVALID;
   if (a.B < 0 || a.H < 0 || a.W < 0) return FIM_ERR_INVALID;
@@ -297,10 +258,7 @@ static int dwpw_launch(const DwPwArgs& a, int kind, int64_t C, int64_t N, hipStr
   t.ntiles = (int64_t)t.tiles_x * t.tiles_y * a.B;
   if (t.ntiles > (1LL << 31) - 8) return FIM_ERR_UNSUPPORTED;
   const dim3 grid((unsigned)(cdiv(t.ntiles, 8) * 8));  // a multiple of the 8 XCDs
-  if (kind == DP_MX)
-    dw_pw_kernel<DP_MX><<<grid, dim3(256), 0, stream>>>(t);
-  else
-    dw_pw_kernel<DP_INT8><<<grid, dim3(256), 0, stream>>>(t);
+  dw_pw_kernel<<<grid, dim3(256), 0, stream>>>(t);
   return launch_status();
 }
 
@@ -313,21 +271,9 @@ int fim_depthwise5x5_relu_pointwise_mxfp8(const uint16_t* x, int64_t B, int64_t 
   if (pw_scale_e8m0 == nullptr || ((uintptr_t)pw_scale_e8m0 % 4) != 0) return FIM_ERR_INVALID;
   if (B > 2147483647LL || H > 2147483647LL || W > 2147483647LL || B * H * W * C >= (1LL << 40))
     return FIM_ERR_UNSUPPORTED;
-  DwPwArgs a{x, dw_weight, dw_bias, pw_weight, pw_scale_e8m0, nullptr, nullptr, pw_bias, pw_bias_dtype, out,
+  DwPwArgs a{x, dw_weight, dw_bias, pw_weight, pw_scale_e8m0, pw_bias, pw_bias_dtype, out,
              (int)B, (int)H, (int)W, 0, 0, 0};
-  return dwpw_launch(a, DP_MX, C, N, stream);
-}
-
-int fim_depthwise5x5_relu_pointwise_int8(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t C,
-                                         const uint16_t* dw_weight, const float* dw_bias, const int8_t* pw_weight,
-                                         int64_t N, const float* pw_wscale, const float* a_scale, const void* pw_bias,
-                                         int pw_bias_dtype, uint16_t* out, hipStream_t stream) {
-  if (pw_wscale == nullptr || a_scale == nullptr) return FIM_ERR_INVALID;
-  if (B > 2147483647LL || H > 2147483647LL || W > 2147483647LL || B * H * W * C >= (1LL << 40))
-    return FIM_ERR_UNSUPPORTED;
-  DwPwArgs a{x, dw_weight, dw_bias, reinterpret_cast<const uint8_t*>(pw_weight), nullptr, pw_wscale, a_scale, pw_bias,
-             pw_bias_dtype, out, (int)B, (int)H, (int)W, 0, 0, 0};
-  return dwpw_launch(a, DP_INT8, C, N, stream);
+  return dwpw_launch(a, C, N, stream);
 }
 
 }  // extern "C"

@@ -191,22 +191,18 @@ int fim_depthwise5x5(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t
                      const float* bias, int act, int out_mode, const float* scale, const int8_t* exponent, void* out,
                      int8_t* exponent_out, uint8_t* swizzled, hipStream_t stream);
 
-/* The depthwise-then-pointwise refiner blocks in one kernel, for C = 128 and a 128 x 128 pointwise weight (the
- * reference's fused shapes; other shapes return 99 and take the two-launch composite). Replace the fused Triton
- * kernels _dw5x5_relu_mx_pointwise_kernel / _dw5x5_relu_int8_pointwise_kernel (flashim/backends/triton/conv.py:310-508)
- * behind ops.depthwise5x5_relu_pointwise_mxfp8 / _int8 (flashim/ops/conv.py:93-138); bit for bit the composite
- * (fim_depthwise5x5 then fim_mxfp8_scaled_mm / fim_int8_linear). x BF16 NHWC [B, H, W, 128] (16-byte aligned);
- * dw_weight BF16 [25, 128]; dw_bias FP32 [128]; pw_weight [128 (n), 128 (k)] E4M3 / INT8; MXFP8: pw_scale_e8m0 [128, 4]
- * E8M0 bytes; INT8: pw_wscale FP32 [128] and the static activation scale a_scale (FP32 scalar); pw_bias [128] FP32 or
- * BF16 (dtype code as fim_int8_linear) or NULL; out BF16 NHWC [B, H, W, 128]. */
+/* The MXFP8 depthwise-then-pointwise refiner block in one kernel, for C = 128 and a 128 x 128 pointwise weight (the
+ * reference's fused shape; other shapes return 99 and take the two-launch composite). Replaces the fused Triton kernel
+ * _dw5x5_relu_mx_pointwise_kernel (flashim/backends/triton/conv.py:310-420) behind
+ * ops.depthwise5x5_relu_pointwise_mxfp8 (flashim/ops/conv.py:93-117); bit for bit the composite (fim_depthwise5x5 then
+ * fim_mxfp8_scaled_mm). x BF16 NHWC [B, H, W, 128] (16-byte aligned); dw_weight BF16 [25, 128]; dw_bias FP32 [128];
+ * pw_weight [128 (n), 128 (k)] E4M3; pw_scale_e8m0 [128, 4] E8M0 bytes; pw_bias [128] FP32 or BF16 (dtype code as
+ * fim_int8_linear) or NULL; out BF16 NHWC [B, H, W, 128]. The INT8 block (flashim/ops/conv.py:119-138) runs as its
+ * two-launch composite, fim_depthwise5x5 then fim_int8_linear. */
 int fim_depthwise5x5_relu_pointwise_mxfp8(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t C,
                                           const uint16_t* dw_weight, const float* dw_bias, const uint8_t* pw_weight,
                                           int64_t N, const uint8_t* pw_scale_e8m0, const void* pw_bias,
                                           int pw_bias_dtype, uint16_t* out, hipStream_t stream);
-int fim_depthwise5x5_relu_pointwise_int8(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t C,
-                                         const uint16_t* dw_weight, const float* dw_bias, const int8_t* pw_weight,
-                                         int64_t N, const float* pw_wscale, const float* a_scale, const void* pw_bias,
-                                         int pw_bias_dtype, uint16_t* out, hipStream_t stream);
 
 /* ---- test hooks ------------------------------------------------------------------------------------------------ */
 
