@@ -33,6 +33,9 @@ PEAK_HBM_GBS = 8000.0
 # scaled by what the counter reads for a plain 64 MiB device copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); the runs and the
 # arithmetic are in profiles/conv_mxfp8_1x1_gelu_cfg2.md. Re-measured by hand when the kernel changes.
 CFG2_TRAFFIC_BYTES = int((6264.1 * 2.0 + 20000.0 * 1.0) * 1024)  # the op's one launch (wide-tile kernel)
+# The config-4 block's algorithmic HBM bytes when fused (204.8 MB for 2 x 400 x 400 x 64: 10 bytes per
+# element); GBps_own_launches divides instead the bytes this library's own launches of the block must move once.
+CFG4_FUSED_BYTES = 204_800_000
 DEV = "cuda"
 
 
@@ -79,18 +82,51 @@ def time_graph(fn, steps: int, warmup: int, per_graph: int = 10) -> float:
     return start.elapsed_time(end) / (replays * per_graph)
 
 
-def time_cpu(fn, budget_s: float = 10.0, max_calls: int = 2000, warmup: int = 2) -> tuple[float, int]:
-    """Median ms of ``fn`` over the calls that fit in ``budget_s`` seconds (at most ``max_calls``; after ``warmup``
-    calls), so the sample is a bounded ~10 s of CPU work whatever the host's speed."""
+def time_graph_cold(fns, steps: int, warmup: int) -> float:
+    """Mean ms per call with a cold working set: ``fns`` are the same op bound to distinct input buffers (together past
+    the 256 MB Infinity Cache), captured back to back in one HIP graph with every output kept alive (so no call
+    reuses another's output memory either), so each call reads and writes memory the previous calls did not touch."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for fn in fns:
+            fn()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph, keep = torch.cuda.CUDAGraph(), []
+    with torch.cuda.graph(graph):
+        for fn in fns:
+            keep.append(fn())
+    replays = max(1, -(-steps // len(fns)))
+    for _ in range(max(1, -(-warmup // len(fns)))):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (replays * len(fns))
+
+
+COLD_BYTES = 300 << 20  # a working set past the 256 MB Infinity Cache
+
+
+def cold_sets(bytes_per_call: int) -> int:
+    return max(2, -(-COLD_BYTES // bytes_per_call))
+
+
+def time_cpu(fn, calls: int = 50, warmup: int = 10) -> float:
+    """Median ms of ``fn`` over ``calls`` calls after ``warmup`` untimed ones."""
     for _ in range(warmup):
         fn()
     samples = []
-    t_end = time.perf_counter() + budget_s
-    while len(samples) < max_calls and (not samples or time.perf_counter() < t_end):
+    for _ in range(calls):
         t0 = time.perf_counter()
         fn()
         samples.append((time.perf_counter() - t0) * 1e3)
-    return statistics.median(samples), len(samples)
+    return statistics.median(samples)
 
 
 # -- workloads -------------------------------------------------------------------------------------------------
@@ -178,7 +214,8 @@ def cfg4_depthwise():
     e = torch.full((2,), -6, dtype=torch.int8, device=DEV)
     fn = lambda: ops.depthwise5x5_gelu(x.permute(0, 3, 1, 2), w, b, exponent=e)  # noqa: E731
     pixels = 2 * 400 * 400
-    return fn, {"bytes": pixels * 64 * 2 + pixels * 64}
+    bind = lambda xi: (lambda: ops.depthwise5x5_gelu(xi.permute(0, 3, 1, 2), w, b, exponent=e))  # noqa: E731
+    return fn, {"bytes": pixels * 64 * 2 + pixels * 64}, (x, bind)
 
 
 def stem():
@@ -234,21 +271,43 @@ def copy_calibration():
 # -- CPU baseline (oracle) ---------------------------------------------------------------------------------------
 
 
-def cpu_baseline_cfg2(args, steps_budget_s: float = 10.0) -> dict:
+def _cpu_threads() -> int:
+    cores = min(os.cpu_count() or 1, 16)  # the GPU box's CPU share is 16 threads, whatever os.cpu_count() reports
+    torch.set_num_threads(cores)
+    return cores
+
+
+def cpu_baseline_cfg2(args) -> dict:
+    """Config 2 through the torch CPU oracle, BASELINE.md's protocol: 10 warm-up calls, median of 50."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import reference as ref
 
-    cores = min(os.cpu_count() or 1, 16)  # the GPU box's CPU share is 16 threads, whatever os.cpu_count() reports
-    torch.set_num_threads(cores)
+    cores = _cpu_threads()
     cpu_args = [a.cpu() if isinstance(a, torch.Tensor) else a for a in args]
-    ms, calls = time_cpu(lambda: ref.mxfp8_conv2d(*cpu_args, gelu=True), budget_s=steps_budget_s)
+    ms = time_cpu(lambda: ref.mxfp8_conv2d(*cpu_args, gelu=True))
     ops = 2 * 20000 * 512 * 512
     return {
         "value": round(ops / (ms * 1e-3) / 1e12, 5), "unit": "TOPS", "cores": cores, "kind": "port",
         "ms": round(ms, 3),
         "sample": f"config 2 in full (M=20000, K=N=512, bias+GELU): oracle.reference.mxfp8_conv2d (torch CPU, "
-                  f"FlashIM's reference path restated), median of {calls} calls "
-                  f"(~{calls * ms / 1e3:.1f} s of CPU work), torch threads={cores}",
+                  f"FlashIM's reference path restated), 10 warm-up calls then the median of 50 "
+                  f"(~{60 * ms / 1e3:.1f} s of CPU work), torch threads={cores}",
+    }
+
+
+def cpu_baseline_cfg1(args) -> dict:
+    """Config 1 (FlashIM's own CPU-runnable case) through the torch CPU oracle, same protocol."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import reference as ref
+
+    cores = _cpu_threads()
+    cpu_args = [a.cpu() if isinstance(a, torch.Tensor) else a for a in args]
+    ms = time_cpu(lambda: ref.int8_conv2d(*cpu_args))
+    ops = 2 * 128 * 128 * 64 * 576
+    return {
+        "value": round(ops / (ms * 1e-3) / 1e12, 5), "unit": "TOPS", "cores": cores, "kind": "port", "ms": round(ms, 3),
+        "sample": f"config 1 in full (INT8 3x3, 1x128x128, 64 -> 64): oracle.reference.int8_conv2d (torch CPU), "
+                  f"10 warm-up calls then the median of 50, torch threads={cores}",
     }
 
 
@@ -295,6 +354,14 @@ def main() -> int:
         results[name] = {"ms": round(ms, 5), "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)}
         return ms
 
+    def cold(name, x, bind, nbytes):
+        """The cold-working-set variant of ``name``: the op over distinct copies of its input ``x``."""
+        fns = [bind(x.clone()) for _ in range(cold_sets(nbytes))]
+        ms = time_graph_cold(fns, steps, warmup)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        results[name].update({"cold_ms": round(ms, 5), "cold_GBps": round(gbs, 1),
+                              "cold_hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "cold_sets": len(fns)})
+
     only = a.only
     c2 = None
     if only in (None, "cfg1"):
@@ -304,15 +371,23 @@ def main() -> int:
         fn, info, c2_args = cfg2()
         c2 = (fn, info, c2_args)
         gemm_line("cfg2_mxfp8_1x1_gelu", fn, info)
+        from flashim_amd import ops as _ops
+        cold("cfg2_mxfp8_1x1_gelu", c2_args[0],
+             lambda xi: (lambda: _ops.mxfp8_conv2d(xi, *c2_args[1:], gelu=True)), info["bytes"])
     if only in (None, "cfg3", "cfg3q"):
-        (conv, cinfo, _), (qfn, qinfo, _) = cfg3()
+        (conv, cinfo, _), (qfn, qinfo, qargs) = cfg3()
         if only in (None, "cfg3"):
             gemm_line("cfg3_mxfp8_3x3_bn_relu", conv, cinfo)
         if only in (None, "cfg3q"):
             hbm_line("cfg3q_quantize_mxfp8", qfn, qinfo)
+            from flashim_amd import ops as _ops
+            x_bf16, q_exp = qargs
+            cold("cfg3q_quantize_mxfp8", x_bf16, lambda xi: (lambda: _ops.quantize_mxfp8(xi, q_exp).values),
+                 qinfo["bytes"])
     if only in (None, "dw"):
-        fn, info = cfg4_depthwise()
+        fn, info, (dw_x, dw_bind) = cfg4_depthwise()
         hbm_line("cfg4_depthwise_gelu_mxfp8", fn, info)
+        cold("cfg4_depthwise_gelu_mxfp8", dw_x, dw_bind, info["bytes"])
     if only in (None, "stem"):
         fn, info = stem()
         hbm_line("stem_conv3x3_cin3_int8", fn, info)
@@ -327,9 +402,11 @@ def main() -> int:
             for preset in ("mxfp8", "int8"):
                 fn, info = blocks.bench_block(preset, device=DEV)
                 ms = time_graph(fn, steps, warmup, per_graph=2)
+                fused_gbs = CFG4_FUSED_BYTES / (ms * 1e-3) / 1e9
                 results[f"cfg4_block_{preset}"] = {
-                    "ms": round(ms, 5), "GBps_unfused_chain": round(info["bytes"] / (ms * 1e-3) / 1e9, 1),
-                    "hbm_frac": round(info["bytes"] / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                    "ms": round(ms, 5), "GBps_fused_algorithmic": round(fused_gbs, 1),
+                    "hbm_frac_fused_algorithmic": round(fused_gbs / PEAK_HBM_GBS, 4),
+                    "GBps_own_launches": round(info["bytes"] / (ms * 1e-3) / 1e9, 1),
                     "TOPS": round(info["ops"] / (ms * 1e-3) / 1e12, 2),
                 }
         for preset in ("int8", "mxfp8"):
@@ -363,6 +440,7 @@ def main() -> int:
     }
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline_cfg2(c2_args)
+        line["cpu_baseline_cfg1"] = cpu_baseline_cfg1(cfg1()[2])
     print(json.dumps(line))
     return 0
 
