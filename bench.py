@@ -254,7 +254,8 @@ def dwpw_block():
                               torch.rand(c, generator=g) * 0.01 + 0.001, pw_b, torch.tensor(0.03))]
     nbytes = 2 * 400 * 400 * c * 2 * 2
     return {
-        "mxfp8_fused": lambda: ops.depthwise5x5_relu_pointwise_mxfp8(*mx),
+        "mxfp8_op": lambda: ops.depthwise5x5_relu_pointwise_mxfp8(*mx),
+        "mxfp8_one_kernel": lambda: hip_conv.pointwise_mxfp8_fused(*mx),
         "mxfp8_composite": lambda: hip_conv.pointwise_mxfp8_composite(*mx),
         "int8_op": lambda: ops.depthwise5x5_relu_pointwise_int8(*i8),
         "int8_composite": lambda: hip_conv.pointwise_int8_composite(*i8),

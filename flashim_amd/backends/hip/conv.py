@@ -169,14 +169,37 @@ def _fused_pointwise_shape(value: Tensor, pw_weight: Tensor) -> bool:
     return value.shape[1] == 128 and tuple(pw_weight.shape) == (128, 128)
 
 
+@torch.compiler.assume_constant_result
+def _compute_units(index: int) -> int:
+    return torch.cuda.get_device_properties(index).multi_processor_count
+
+
+def _composite_gemm_is_pointwise_kernel(value: Tensor) -> bool:
+    """Whether the composite's 128-channel GEMM has at least two 256-row tiles per CU, the condition under which the
+    library runs it on its register-operand pointwise kernel: then the two launches are the faster (at 2 x 128 x
+    400 x 400 on MI355X: 89.7 against 94.3 us for the one-kernel block)."""
+    batch, _, height, width = value.shape
+    index = value.device.index if value.device.index is not None else torch.cuda.current_device()
+    return -(-(batch * height * width) // 256) >= 2 * _compute_units(index)
+
+
 def depthwise5x5_relu_pointwise_mxfp8(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
                                       pw_scale_swizzled: Tensor, pw_scale_u8: Tensor, pw_bias: Tensor) -> Tensor:
     """The MXFP8 refiner block (``flashim/ops/conv.py:93-113``) -> ``[B, C, H, W]`` view of NHWC BF16. At 128 x 128
-    one kernel (``fim_depthwise5x5_relu_pointwise_mxfp8``: the quantized activations stay on chip), else the
-    composite."""
-    if not _fused_pointwise_shape(value, pw_weight):
+    one kernel (``fim_depthwise5x5_relu_pointwise_mxfp8``: the quantized activations stay on chip) unless the image is
+    large enough for the composite's GEMM to run on the pointwise kernel; otherwise the composite."""
+    if not _fused_pointwise_shape(value, pw_weight) or _composite_gemm_is_pointwise_kernel(value):
         return pointwise_mxfp8_composite(value, dw_weight, dw_bias, pw_weight, pw_scale_swizzled, pw_scale_u8,
                                          pw_bias)
+    return pointwise_mxfp8_fused(value, dw_weight, dw_bias, pw_weight, pw_scale_swizzled, pw_scale_u8, pw_bias)
+
+
+def pointwise_mxfp8_fused(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
+                          pw_scale_swizzled: Tensor, pw_scale_u8: Tensor, pw_bias: Tensor) -> Tensor:
+    """One kernel at C = 128 with a 128 x 128 pointwise weight; bit for bit the composite."""
+    if not _fused_pointwise_shape(value, pw_weight):
+        raise ValueError(f"the one-kernel block needs C = 128 and a 128 x 128 weight, got {tuple(value.shape)}, "
+                         f"{tuple(pw_weight.shape)}")
     x, dw_w, dw_b = _dw_operands(value, dw_weight, dw_bias)
     out = library.depthwise5x5_relu_pointwise_mxfp8(
         x, dw_w, dw_b, pw_weight.contiguous().view(torch.uint8),

@@ -1524,7 +1524,9 @@ static int launch_patch(ConvArgs a, hipStream_t stream) {
 // tile's rows), runs 2 x 8 blocks of 16 x 16 against the LDS weights, and writes
 // its epilogue through a private LDS staging area in whole lines. Two wavefronts per SIMD drift apart, so one's loads
 // and MFMAs run while the other's epilogue keeps the VALU busy.
-template <int KIND, int OUT, int KS>
+// XS = 1: MXFP8 activations with per-row E8M0 scales in the 128x4 swizzled layout (mxfp8_scaled_mm's dynamic
+// quantization), read per tile with the rows; XS = 0: per-channel-block exponents.
+template <int KIND, int OUT, int KS, int XS = 0>
 __global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
   constexpr int BN = 128, MB = 2, NB = 8, TMW = MB * 16;  // a wavefront's tile: 32 pixels x 128 channels
   constexpr int WTS_BYTES = KS * BN * KC;                // [K step][channel][128 B]
@@ -1594,18 +1596,27 @@ __global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
 #pragma unroll
     for (int i = 0; i < WEXP_PASSES; ++i)
       if (tid + 512 * i < WEXP_N) wexp_s[tid + 512 * i] = (uint8_t)e[i];
-    if (tid < KS * 4) xexp_s[tid] = (uint8_t)((int)a.x_expo[tid] + 127);
+    if (XS == 0 && tid < KS * 4) xexp_s[tid] = (uint8_t)((int)a.x_expo[tid] + 127);
   }
 
   // activation operands straight from global memory: block j, K step ks is the lane's row's bytes [16 g, +16) and
   // [64 + 16 g, +16) of the step (rows past M read as zero)
   const __amdgpu_buffer_rsrc_t xr =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.x), (short)0, x_nrec, 0x00020000);
-  auto load_x = [&](int t, v8i (&xa)[MB][KS]) __attribute__((always_inline)) {
+  auto load_x = [&](int t, v8i (&xa)[MB][KS], int (&sr)[MB][KS]) __attribute__((always_inline)) {
     const int m0 = (t / a.n_tiles) * (8 * TMW) + wave * TMW;
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
       const int m = m0 + j * 16 + (lane & 15);
+      if constexpr (XS == 1) {  // the row's E8M0 byte of K block 4 ks + g
+        const int r = m < a.M ? m : a.M - 1, rt = r & 127;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const int cb = 4 * ks + g;
+          sr[j][ks] = (int)a.x_swz[(((int64_t)(r >> 7) * a.x_swz_tiles_k + (cb >> 2)) << 9) + (rt & 31) * 16 +
+                                   (rt >> 5) * 4 + (cb & 3)];
+        }
+      }
       const uint32_t base = m < a.M ? (uint32_t)(m * a.Cin + 16 * g) : OOB;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
@@ -1635,7 +1646,7 @@ __global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
   if constexpr (KIND == KIND_MX) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      sxs[ks] = xexp_s[ks * 4 + g];
+      sxs[ks] = XS == 0 ? (int)xexp_s[ks * 4 + g] : 127;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         uint32_t packed = 0;
@@ -1658,7 +1669,8 @@ __global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
   // one tile: its operand loads are waited for right away; the other wavefront on the SIMD runs meanwhile
   auto run_tile = [&](int t) __attribute__((always_inline)) {
     v8i xc[MB][KS];
-    load_x(t, xc);
+    int sr[MB][KS];  // per-row scales (XS = 1)
+    load_x(t, xc, sr);
     int wq[NB];  // weight offsets made opaque per tile (else all K steps' weight operands are hoisted)
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
@@ -1693,7 +1705,8 @@ __global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
                                                                 __builtin_shufflevector(xc[j][ks], xc[j][ks], 4, 5, 6, 7),
                                                                 acc_i[i][j], 0, 0, 0);
           } else {
-            acc_f[i][j] = mfma_scale_opsel(w, xc[j][ks], acc_f[i][j], i & 3, swp[ks][i >> 2], sxs[ks]);
+            acc_f[i][j] = mfma_scale_opsel(w, xc[j][ks], acc_f[i][j], i & 3, swp[ks][i >> 2],
+                                           XS == 1 ? sr[j][ks] : sxs[ks]);
           }
         }
       }
@@ -1752,7 +1765,7 @@ __global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
 // Whether the pointwise kernel applies: 1 x 1, stride 1, no padding, 128 <= Cin <= 512 with Cin % 128 == 0,
 // Cout >= 128 (Cout % 16 == 0 by the fast epilogue), dense 16-byte aligned output, no pooling / per-row scales.
 static int pw_ks(const ConvArgs& a, int lw, bool fast_ok) {
-  if (lw != 16 || !fast_ok || a.x_swz != nullptr || a.pool_out != nullptr || a.a_scale_rows != nullptr) return 0;
+  if (lw != 16 || !fast_ok || a.pool_out != nullptr || a.a_scale_rows != nullptr) return 0;
   if (a.kh != 1 || a.kw != 1 || a.sh != 1 || a.sw != 1 || a.ph != 0 || a.pw != 0) return 0;
   if (a.Cin % KC != 0 || a.Cin > 4 * KC || a.Cout < 128 || ((uintptr_t)a.out & 15) != 0 || a.out_ld != a.Cout)
     return 0;
@@ -1764,14 +1777,25 @@ static int pw_ks(const ConvArgs& a, int lw, bool fast_ok) {
   return a.Cin / KC;
 }
 
+template <int KIND, int OUT, int XS>
+static void launch_pw_ks(const ConvArgs& a, int ks, dim3 grid, hipStream_t stream) {
+  switch (ks) {
+    case 1: conv_pw_kernel<KIND, OUT, 1, XS><<<grid, dim3(512), 0, stream>>>(a); break;
+    case 2: conv_pw_kernel<KIND, OUT, 2, XS><<<grid, dim3(512), 0, stream>>>(a); break;
+    case 3: conv_pw_kernel<KIND, OUT, 3, XS><<<grid, dim3(512), 0, stream>>>(a); break;
+    default: conv_pw_kernel<KIND, OUT, 4, XS><<<grid, dim3(512), 0, stream>>>(a); break;
+  }
+}
+
 template <int KIND, int OUT>
 static void launch_pw_out(const ConvArgs& a, int ks, dim3 grid, hipStream_t stream) {
-  switch (ks) {
-    case 1: conv_pw_kernel<KIND, OUT, 1><<<grid, dim3(512), 0, stream>>>(a); break;
-    case 2: conv_pw_kernel<KIND, OUT, 2><<<grid, dim3(512), 0, stream>>>(a); break;
-    case 3: conv_pw_kernel<KIND, OUT, 3><<<grid, dim3(512), 0, stream>>>(a); break;
-    default: conv_pw_kernel<KIND, OUT, 4><<<grid, dim3(512), 0, stream>>>(a); break;
+  if constexpr (KIND == KIND_MX) {
+    if (a.x_swz != nullptr) {
+      launch_pw_ks<KIND, OUT, 1>(a, ks, grid, stream);
+      return;
+    }
   }
+  launch_pw_ks<KIND, OUT, 0>(a, ks, grid, stream);
 }
 
 template <int KIND>

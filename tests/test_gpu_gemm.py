@@ -107,7 +107,10 @@ def test_mxfp8_linear(rows, k, n, has_bias):
     _assert_mx_close(got, want)
 
 
-@pytest.mark.parametrize("m,k,n", [(1, 32, 32), (300, 256, 96), (4096, 128, 128), (1000, 512, 320)])
+# the last three have at least two 256-row tiles per CU (256 CUs) and run the register-operand pointwise kernel with
+# per-row swizzled scales; the others the one-round kernels
+@pytest.mark.parametrize("m,k,n", [(1, 32, 32), (300, 256, 96), (4096, 128, 128), (1000, 512, 320),
+                                   (140000, 128, 128), (70000, 256, 256), (40001, 512, 512)])
 @pytest.mark.parametrize("has_bias", [False, True])
 def test_mxfp8_scaled_mm(m, k, n, has_bias):
     g = torch.Generator().manual_seed(m + n)
@@ -205,7 +208,7 @@ def test_fused_depthwise_pointwise_matches_composite(batch, hw, bias):
     dev = lambda ts: [t.to(DEV) if t is not None else None for t in ts]  # noqa: E731
     pw_w, pw_e = ref.quantized_weight_from_float(torch.randn(channels, channels, generator=g) * 0.1)
     args = dev((x, dw_w, dw_b, pw_w, ref.swizzle_scales(pw_e), ref.exponent_to_e8m0(pw_e), pw_b))
-    fused = ops.depthwise5x5_relu_pointwise_mxfp8.get("hip")(*args)
+    fused = hip_conv.pointwise_mxfp8_fused(*args)
     composite = hip_conv.pointwise_mxfp8_composite(*args)
     assert fused.shape == composite.shape == (batch, channels, *hw)
     assert torch.equal(fused.view(torch.int16), composite.view(torch.int16))
