@@ -70,17 +70,10 @@ __device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float
 #endif
 }
 
-// E4M3 codes of BF16(a..d) * 2^-e, clamped to +-448: the BF16 rounding then static MXFP8 quantize of the references
-// (a BF16 activation quantized with quant/tensor.py:97-121). scale = 2^e, bound = 448 * 2^e. The clamp commutes with
-// the BF16 rounding (bound is a BF16 value and rounding is monotonic), so the values are clamped in FP32 (IEEE
-// minimum / maximum: NaN stays NaN), rounded to BF16 by the pack, and v_cvt_scalef32_pk_fp8_bf16 divides by the scale
-// and converts: 2 operations per value fewer than unpacking, multiplying and converting from FP32, and byte for byte
-// the same codes (measured on the GPU over every BF16 input, NaN and infinities included, at exponents -10..10).
-__device__ __forceinline__ uint32_t e4m3x4_of_bf16(float a, float b, float c, float d, float scale, float bound) {
-  a = __builtin_elementwise_maximum(__builtin_elementwise_minimum(a, bound), -bound);
-  b = __builtin_elementwise_maximum(__builtin_elementwise_minimum(b, bound), -bound);
-  c = __builtin_elementwise_maximum(__builtin_elementwise_minimum(c, bound), -bound);
-  d = __builtin_elementwise_maximum(__builtin_elementwise_minimum(d, bound), -bound);
+// E4M3 codes of BF16(a..d) * 2^-e for values already within +-448 * 2^e (scale = 2^e): the pack rounds to BF16 and
+// v_cvt_scalef32_pk_fp8_bf16 divides by the scale and converts (RNE). Out-of-range values become NaN codes (the
+// conversion does not saturate), so callers clamp first.
+__device__ __forceinline__ uint32_t e4m3x4_of_bf16_inrange(float a, float b, float c, float d, float scale) {
 #ifdef FIM_SOFTWARE_E4M3
   round_bf16x2(a, b);
   round_bf16x2(c, d);
@@ -97,6 +90,20 @@ __device__ __forceinline__ uint32_t e4m3x4_of_bf16(float a, float b, float c, fl
 #endif
 }
 
+// E4M3 codes of BF16(a..d) * 2^-e, clamped to +-448: the BF16 rounding then static MXFP8 quantize of the references
+// (a BF16 activation quantized with quant/tensor.py:97-121). scale = 2^e, bound = 448 * 2^e. The clamp commutes with
+// the BF16 rounding (bound is a BF16 value and rounding is monotonic), so the values are clamped in FP32 (IEEE
+// minimum / maximum: NaN stays NaN), rounded to BF16 by the pack, and v_cvt_scalef32_pk_fp8_bf16 divides by the scale
+// and converts: 2 operations per value fewer than unpacking, multiplying and converting from FP32, and byte for byte
+// the same codes (measured on the GPU over every BF16 input, NaN and infinities included, at exponents -10..10).
+__device__ __forceinline__ uint32_t e4m3x4_of_bf16(float a, float b, float c, float d, float scale, float bound) {
+  a = __builtin_elementwise_maximum(__builtin_elementwise_minimum(a, bound), -bound);
+  b = __builtin_elementwise_maximum(__builtin_elementwise_minimum(b, bound), -bound);
+  c = __builtin_elementwise_maximum(__builtin_elementwise_minimum(c, bound), -bound);
+  d = __builtin_elementwise_maximum(__builtin_elementwise_minimum(d, bound), -bound);
+  return e4m3x4_of_bf16_inrange(a, b, c, d, scale);
+}
+
 __device__ __forceinline__ uint8_t e4m3(float a) {
 #ifdef FIM_SOFTWARE_E4M3
   return f32_to_e4m3_sw(a);
@@ -105,18 +112,23 @@ __device__ __forceinline__ uint8_t e4m3(float a) {
 #endif
 }
 
-// GELU, erf form: 0.5 x erfc(-x / sqrt 2) = x - h (x >= 0) or h (x < 0), h = x * erfc(|x| / sqrt 2) / 2. With
-// z = min(|x| / sqrt 2, 4.1) and t = 2 z / 4.1 - 1, log2(erfc(z) / 2) is the degree-8 polynomial P(t) below (Chebyshev
-// fit of log2 erfc on [0, 4.1], minus 1), so h = x * 2^P(t): one v_exp_f32, 8 FMAs, no division. x < -5.53125 gives
-// -0 as torch does (ATen's FP32 1 + erf(x / sqrt 2) is exactly 0 there). Against torch's BF16 GELU it differs in
-// 0.96% of the finite BF16 inputs, by one BF16 step (torch's own erf rounding moves values across BF16 rounding
-// boundaries too); in torch's cancelling negative tail (x < -3) both are within 2^-12 of each other.
+// GELU, erf form: 0.5 x erfc(-x / sqrt 2) = max(x, 0) - |x| E with E = erfc(|x| / sqrt 2) / 2 (x >= 0: x - x E;
+// x < 0: x E). With z = |x| / sqrt 2 and t = 2 z / 4.1 - 1, log2 E is the degree-8 polynomial P(t) below (Chebyshev
+// fit of log2 erfc on [0, 4.1], minus 1), so E = 2^P(t): one v_exp_f32, 8 FMAs, no division, and the last step is one
+// FMA, fma(-|x|, E, max(x, -0)). The polynomial needs no clamp outside the fit: P is monotonically decreasing for
+// t > 1 and stays within 0.5 of log2 E up to |x| = 10 (E < 2^-77 there; P reaches -880 at |x| = 20 and -inf once its
+// leading term overflows), so the large-|x| limits come out right by themselves: x - 0 = x for large positive x, and
+// -0 (fma(-|x|, 0, -0)) once 2^P underflows for large negative x. Between x = -5.53 (where torch's FP32 1 + erf(x / sqrt 2)
+// becomes exactly 0, so torch returns -0) and about x = -12 the result is the true tiny GELU value (< 1e-7 in magnitude)
+// instead of -0. Against torch's BF16 GELU it differs by one BF16 step in about 1% of the finite BF16 inputs (torch's own
+// erf rounding moves values across BF16 rounding boundaries too); in torch's cancelling negative tail (x < -3) both are
+// within 2^-12 of each other. Signed zeros follow torch: GELU(+0) = +0, GELU(-0) = -0.
 __device__ __forceinline__ float gelu_erf(float x) {
   // Evaluated in the rescaled variable u = s t, s = |c8|^(1/8) = 0.3224875, so the polynomial is monic up to sign
   // (coefficients c_k / s^k): its first Horner step is one subtraction with one literal (no constant kept in a
-  // register). u = min(|x| / sqrt 2, 4.1) * 2 s / 4.1 - s as one FMA and a clamp at u = s.
+  // register). u = |x| / sqrt 2 * 2 s / 4.1 - s as one FMA.
   constexpr float kS = 0.3224875f;
-  const float u = fminf(fmaf(fabsf(x), 0.70710678118654752440f * 0.48780487804878f * kS, -kS), kS);
+  const float u = fmaf(fabsf(x), 0.70710678118654752440f * 0.48780487804878f * kS, -kS);
   float p = -9.393265f - u;
   p = fmaf(p, u, 13.051149f);
   p = fmaf(p, u, -10.621295f);
@@ -125,12 +137,7 @@ __device__ __forceinline__ float gelu_erf(float x) {
   p = fmaf(p, u, -53.993702f);
   p = fmaf(p, u, -41.367184f);
   p = fmaf(p, u, -9.062012672f);  // the fit's constant -8.062 minus 1: the factor 1/2
-  // Below -5.53125 the exponent goes to -inf (the clamp argument is negative and scaled by 2^30 far past -149), so
-  // h = x * 0 = -0. h carries the sign of x, so x - h (x >= 0) and h (x < 0) are both max(x, -0) - |h|: no compare,
-  // no select, and the sign of zero follows torch (GELU(-0) = -0, the negative tail is -0).
-  p = fminf(p, fmaf(x, 0x1p30f, 5.53125f * 0x1p30f));
-  const float h = x * __builtin_amdgcn_exp2f(p);
-  return __builtin_elementwise_maximum(x, -0.0f) - fabsf(h);
+  return fmaf(-fabsf(x), __builtin_amdgcn_exp2f(p), __builtin_elementwise_maximum(x, -0.0f));
 }
 
 // gelu_erf over N independent values, written step by step (each Horner step over all N values before the next), so
@@ -142,7 +149,7 @@ __device__ __forceinline__ void gelu_erf_n(float (&x)[N]) {
   constexpr float kC[7] = {13.051149f, -10.621295f, 7.961414f, -5.8366094f, -53.993702f, -41.367184f, -9.062012672f};
   float u[N], p[N];
 #pragma unroll
-  for (int i = 0; i < N; ++i) u[i] = fminf(fmaf(fabsf(x[i]), 0.70710678118654752440f * 0.48780487804878f * kS, -kS), kS);
+  for (int i = 0; i < N; ++i) u[i] = fmaf(fabsf(x[i]), 0.70710678118654752440f * 0.48780487804878f * kS, -kS);
 #pragma unroll
   for (int i = 0; i < N; ++i) p[i] = -9.393265f - u[i];
 #pragma unroll
@@ -150,11 +157,7 @@ __device__ __forceinline__ void gelu_erf_n(float (&x)[N]) {
 #pragma unroll
     for (int i = 0; i < N; ++i) p[i] = fmaf(p[i], u[i], kC[k]);
 #pragma unroll
-  for (int i = 0; i < N; ++i) p[i] = fminf(p[i], fmaf(x[i], 0x1p30f, 5.53125f * 0x1p30f));
-#pragma unroll
-  for (int i = 0; i < N; ++i) p[i] = x[i] * __builtin_amdgcn_exp2f(p[i]);
-#pragma unroll
-  for (int i = 0; i < N; ++i) x[i] = __builtin_elementwise_maximum(x[i], -0.0f) - fabsf(p[i]);
+  for (int i = 0; i < N; ++i) x[i] = fmaf(-fabsf(x[i]), __builtin_amdgcn_exp2f(p[i]), __builtin_elementwise_maximum(x[i], -0.0f));
 }
 
 // Workgroup barrier for LDS hand-offs that leaves global loads in flight: waits only for this wave's LDS operations

@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256, 2) void dw_pw_kernel(const DwPwArgs a) {
 
     v4f acc[8];  // [column quad cq]: D[i = 0..3][j = r4] = output (row 4 rq + r4, column 4 cq + i)
 #pragma unroll
-    for (int cq = 0; cq < 8; ++cq) acc[cq] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int cq = 0; cq < 8; ++cq) acc[cq] = v4f{dbias, dbias, dbias, dbias};  // the bias first, as depthwise.hip
     const uint32_t* plane = &sm[(16 * cg + bch) * DP_PLANE];
 #pragma unroll
     for (int ky = 0; ky < 5; ++ky) {
@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256, 2) void dw_pw_kernel(const DwPwArgs a) {
 #pragma unroll
     for (int cq = 0; cq < 8; ++cq)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) y[cq][i] = fmaxf(acc[cq][i] + dbias, 0.f);
+      for (int i = 0; i < 4; ++i) y[cq][i] = fmaxf(acc[cq][i], 0.f);
 
 #pragma unroll
     for (int half = 0; half < 2; ++half) {

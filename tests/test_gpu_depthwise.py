@@ -51,7 +51,7 @@ def test_depthwise_relu_int8(batch, channels, hw):
     assert (got.int() - want.int()).abs().max() <= 1 and (got != want).float().mean() < 5e-3
 
 
-@pytest.mark.parametrize("mode", ["bf16", "int8", "mxfp8"])
+@pytest.mark.parametrize("mode", ["bf16", "int8", "mxfp8", "mxfp8_tiny_scale"])
 @pytest.mark.parametrize("batch,channels,hw", [(2, 64, (40, 37)), (1, 256, (9, 20)), (2, 32, (3, 3))])
 def test_depthwise_gelu(batch, channels, hw, mode):
     x, w, b = _inputs(batch, channels, hw, seed=2)
@@ -60,6 +60,8 @@ def test_depthwise_gelu(batch, channels, hw, mode):
         kwargs["scale"] = torch.tensor(0.02)
     elif mode == "mxfp8":
         kwargs["exponent"] = torch.full((channels // 32,), -5, dtype=torch.int8)
+    elif mode == "mxfp8_tiny_scale":  # a bound of 448 * 2^-13 < 0.17: GELU's negative values saturate too (the kernel's two-sided clamp)
+        kwargs["exponent"] = torch.full((channels // 32,), -13, dtype=torch.int8)
     got = ops.depthwise5x5_gelu.get("hip")(x.to(DEV), w.to(DEV), b.to(DEV),
                                             **{k: v.to(DEV) for k, v in kwargs.items()}).cpu()
     want = ref.depthwise5x5_gelu(x, w, b, **kwargs)
@@ -67,8 +69,13 @@ def test_depthwise_gelu(batch, channels, hw, mode):
     if mode == "bf16":
         diff = (got.float() - want.float()).abs()
         # GELU's tail (x < -3) is tiny and computed through erfc here, through 1 + erf (cancelling) in torch:
-        # an absolute floor of 2^-12 covers it, everything else is within one BF16 rounding
-        assert (diff <= want.float().abs() * 2**-7 + 2**-12).all()
+        # an absolute floor of 2^-12 covers it, everything else is within one BF16 rounding. The FP32 sum of the
+        # 25 taps and the bias runs in another order than torch's CPU conv, so a pre-activation value within an FP32
+        # ulp or two of a BF16 rounding boundary can round to the neighbouring BF16 input, which GELU (slope <= 1.13)
+        # carries to at most two output steps: allowed for 1e-4 of the elements.
+        one_step = diff <= want.float().abs() * 2**-7 + 2**-12
+        assert (diff <= want.float().abs() * 2**-6 + 2**-12).all()
+        assert (~one_step).float().mean() <= 1e-4
     elif mode == "int8":
         assert (got.int() - want.int()).abs().max() <= 1 and (got != want).float().mean() < 5e-3
     else:
