@@ -19,7 +19,7 @@ CSRC = PACKAGE / "csrc"
 BUILD = PACKAGE / "_build"
 LIBRARY = PACKAGE / "libflashim_amd.so"
 HOST_LIBRARY = PACKAGE / "libfim_host.so"
-DEVICE_SOURCES = ("quantize.hip", "igemm.hip", "depthwise.hip", "dwpw.hip", "mlp.hip", "stem.hip", "misc.hip")
+DEVICE_SOURCES = ("quantize.hip", "igemm.hip", "depthwise.hip", "dwpw.hip", "mlp.hip", "stem.hip", "pointwise.hip", "misc.hip")
 ARCH = os.environ.get("FLASHIM_AMD_ARCH", "gfx950")
 HIP_FLAGS = (
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract=off", "-munsafe-fp-atomics",

@@ -7,6 +7,8 @@
   MXFP8 out) -> ``fim_depthwise5x5``
 * ``conv2d_small_cin_quantize_int8`` (``flashim/ops/conv.py:225-235``) -> ``fim_conv3x3_small_cin_quantize_int8``
 * ``bias_relu_quantize_int8`` (``flashim/ops/quantize.py:134-142``) -> ``fim_bias_relu_quantize_int8``
+* ``depthwise5x5_relu_pointwise`` (``flashim/ops/conv.py:67-84``, BF16) -> the producer's ReLU + BF16 mode then
+  ``fim_pointwise_bf16``
 * ``depthwise5x5_relu_pointwise_mxfp8`` (``flashim/ops/conv.py:93-113``) -> at C = 128 with a 128 x 128 pointwise
   weight ``fim_depthwise5x5_relu_pointwise_mxfp8`` (one kernel, the reference's fused shapes
   ``flashim/backends/triton/conv.py:310-508``), else the producer then ``fim_mxfp8_scaled_mm``
@@ -183,6 +185,18 @@ def _composite_gemm_is_pointwise_kernel(value: Tensor) -> bool:
     return -(-(batch * height * width) // 256) >= 2 * _compute_units(index)
 
 
+def depthwise5x5_relu_pointwise(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
+                                pw_bias: Tensor) -> Tensor:
+    """The BF16 refiner block (``flashim/ops/conv.py:67-84``) -> ``[B, C_out, H, W]`` view of NHWC BF16 (channels-last
+    memory): the depthwise producer's ReLU + BF16 mode (``relu(dwconv + bias)`` rounded to BF16, the reference's hidden
+    tensor), then the BF16 pointwise GEMM with FP32 accumulation and bias."""
+    batch, _, height, width = value.shape
+    hidden = library.depthwise5x5(*_dw_operands(value, dw_weight, dw_bias), 0, library.DW_BF16, None, None)
+    out = library.pointwise_bf16(hidden, pw_weight.to(device=value.device, dtype=torch.bfloat16).contiguous(),
+                                 pw_bias.to(device=value.device, dtype=torch.float32).contiguous())
+    return out.reshape(batch, height, width, -1).permute(0, 3, 1, 2)
+
+
 def depthwise5x5_relu_pointwise_mxfp8(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
                                       pw_scale_swizzled: Tensor, pw_scale_u8: Tensor, pw_bias: Tensor) -> Tensor:
     """The MXFP8 refiner block (``flashim/ops/conv.py:93-113``) -> ``[B, C, H, W]`` view of NHWC BF16. At 128 x 128
@@ -281,6 +295,17 @@ def eligible_depthwise(value: Tensor, weight: Tensor, bias: Tensor, *rest, **kwa
 
 def eligible_im2col(x, kh, kw, sh, sw, ph, pw, dh, dw) -> bool:
     return isinstance(x, Tensor) and is_gfx950(x.device) and x.ndim == 4 and x.element_size() == 1
+
+
+def eligible_pointwise_bf16(value, dw_weight, dw_bias, pw_weight, pw_bias) -> bool:
+    """The reference's fused-block contract (``flashim/backends/triton/conv.py:540-553``: BF16 weights) on this
+    backend's kernels: C a multiple of 32 up to 128, C_out a multiple of 16 up to 128."""
+    return (
+        eligible_depthwise(value, dw_weight, dw_bias) and value.shape[1] <= 128 and dw_weight.dtype == torch.bfloat16
+        and pw_weight.dtype == torch.bfloat16 and pw_weight.ndim == 2 and pw_weight.shape[1] == value.shape[1]
+        and pw_weight.shape[0] % 16 == 0 and pw_weight.shape[0] <= 128
+        and pw_bias is not None and pw_bias.numel() == pw_weight.shape[0]
+    )
 
 
 def eligible_pointwise_mxfp8(value, dw_weight, dw_bias, pw_weight, pw_scale_swizzled, pw_scale_u8, pw_bias) -> bool:

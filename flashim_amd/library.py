@@ -453,3 +453,19 @@ def bias_relu_quantize_int8(raw: Tensor, bias: Tensor, scale: Tensor) -> Tensor:
 def _(raw, bias, scale):
     b, c, h, w = raw.shape
     return raw.new_empty((b, h, w, c), dtype=torch.int8)
+
+
+@torch.library.custom_op(f"{NS}::pointwise_bf16", mutates_args=())
+def pointwise_bf16(x: Tensor, weight: Tensor, bias: Optional[Tensor]) -> Tensor:
+    """``x`` BF16 ``[M, K]`` times ``weight`` BF16 ``[N, K]`` transposed, plus FP32 ``bias`` -> BF16 ``[M, N]``."""
+    m, k = x.shape
+    n = weight.shape[0]
+    out = torch.empty(m, n, device=x.device, dtype=torch.bfloat16)
+    _lib.call("fim_pointwise_bf16", x.data_ptr(), m, k, weight.data_ptr(), n, _ptr(bias), out.data_ptr(), _stream(x),
+              what=f"pointwise_bf16 {m}x{k}x{n}")
+    return out
+
+
+@pointwise_bf16.register_fake
+def _(x, weight, bias):
+    return x.new_empty((x.shape[0], weight.shape[0]), dtype=torch.bfloat16)

@@ -26,6 +26,7 @@ int8_conv2d = Op("int8_conv2d")
 mxfp8_conv2d = Op("mxfp8_conv2d")
 depthwise5x5_relu_mxfp8 = Op("depthwise5x5_relu_mxfp8")
 depthwise5x5_relu_int8 = Op("depthwise5x5_relu_int8")
+depthwise5x5_relu_pointwise = Op("depthwise5x5_relu_pointwise")
 depthwise5x5_relu_pointwise_mxfp8 = Op("depthwise5x5_relu_pointwise_mxfp8")
 depthwise5x5_relu_pointwise_int8 = Op("depthwise5x5_relu_pointwise_int8")
 im2col_gather = Op("im2col_gather")
@@ -57,6 +58,7 @@ IMPLS = (
      _conv.eligible_depthwise),
     ("depthwise5x5_relu_int8", _conv.depthwise5x5_relu_int8, (Feature.HIP,), _conv.eligible_depthwise),
     ("depthwise5x5_gelu", _conv.depthwise5x5_gelu, (Feature.HIP,), _conv.eligible_depthwise),
+    ("depthwise5x5_relu_pointwise", _conv.depthwise5x5_relu_pointwise, (Feature.HIP,), _conv.eligible_pointwise_bf16),
     ("depthwise5x5_relu_pointwise_mxfp8", _conv.depthwise5x5_relu_pointwise_mxfp8, _MX,
      _conv.eligible_pointwise_mxfp8),
     ("depthwise5x5_relu_pointwise_int8", _conv.depthwise5x5_relu_pointwise_int8, _I8, _conv.eligible_pointwise_int8),

@@ -130,6 +130,7 @@ def impls(upstream_tensor_module) -> dict[str, tuple[Callable, Callable]]:
         "mxfp8_conv2d": (_conv.mxfp8_conv2d, _conv.eligible_mxfp8_conv2d),
         "depthwise5x5_relu_mxfp8": (_conv.depthwise5x5_relu_mxfp8, _conv.eligible_depthwise),
         "depthwise5x5_relu_int8": (_conv.depthwise5x5_relu_int8, _conv.eligible_depthwise),
+        "depthwise5x5_relu_pointwise": (_conv.depthwise5x5_relu_pointwise, _conv.eligible_pointwise_bf16),
         "depthwise5x5_relu_pointwise_mxfp8": (_conv.depthwise5x5_relu_pointwise_mxfp8,
                                               _conv.eligible_pointwise_mxfp8),
         "depthwise5x5_relu_pointwise_int8": (_conv.depthwise5x5_relu_pointwise_int8, _conv.eligible_pointwise_int8),

@@ -361,6 +361,18 @@ def depthwise5x5_gelu(value: Tensor, weight: Tensor, bias: Tensor, *, scale: Ten
     return rows.contiguous()
 
 
+def depthwise5x5_relu_pointwise(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
+                                pw_bias: Tensor) -> Tensor:
+    """ops/conv.py:67-81: BF16 depthwise 5x5 + bias + ReLU (FP32 accumulate) rounded to BF16, then the 1x1 conv with
+    the [C_out, C_in] weight and bias in FP32, rounded to BF16; a [B, C_out, H, W] view of NHWC BF16."""
+    channels = value.shape[1]
+    kernel = dw_weight.float().t().reshape(channels, 1, 5, 5)
+    hidden = F.conv2d(value.to(torch.bfloat16).float(), kernel, dw_bias.float(), padding=2, groups=channels)
+    hidden = F.relu(hidden).to(torch.bfloat16).float()
+    out = F.conv2d(hidden, pw_weight.float()[:, :, None, None], pw_bias.float())
+    return out.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
+
+
 def depthwise5x5_relu_pointwise_mxfp8(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
                                       pw_scale_swizzled: Tensor, pw_scale_u8: Tensor, pw_bias: Tensor) -> Tensor:
     """ops/conv.py:93-107: the dynamic MXFP8 producer then mxfp8_scaled_mm; a [B, C, H, W] view of NHWC BF16."""

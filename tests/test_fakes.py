@@ -119,6 +119,9 @@ def test_gemm_and_block_fakes_match_oracle_shapes():
                                                  ref.exponent_to_e8m0(pe), torch.randn(64))
     assert _fake_run(hc.depthwise5x5_relu_pointwise_mxfp8, value, dw_w, dw_b, pw, ref.swizzle_scales(pe),
                      ref.exponent_to_e8m0(pe), torch.randn(64)) == _sig(want)
+    pw16, pb16 = torch.randn(48, 64).to(torch.bfloat16), torch.randn(48).to(torch.bfloat16)
+    assert _fake_run(hc.depthwise5x5_relu_pointwise, value, dw_w, dw_b, pw16, pb16) == \
+        _sig(ref.depthwise5x5_relu_pointwise(value, dw_w, dw_b, pw16, pb16))
     raw = torch.randn(1, 16, 5, 6).to(torch.bfloat16)
     assert _fake_run(hc.bias_relu_quantize_int8, raw, torch.randn(16), torch.tensor(0.1)) == \
         _sig(ref.bias_relu_quantize_int8(raw, torch.randn(16), torch.tensor(0.1)))

@@ -75,3 +75,5 @@ def test_compile_depthwise_and_blocks():
     w8 = torch.randint(-127, 128, (c, c), dtype=torch.int8, generator=g).to(DEV)
     ws = (torch.rand(c, generator=g) * 0.01 + 0.001).to(DEV)
     _check(lambda v: ops.depthwise5x5_relu_pointwise_int8(v, dw_w, dw_b, w8, ws, pw_b, s), x)
+    pw16 = (torch.randn(c, c, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+    _check(lambda v: ops.depthwise5x5_relu_pointwise(v, dw_w, dw_b, pw16, pw_b), x)

@@ -460,6 +460,30 @@ def test_pointwise_composites_against_float64_on_the_producer_codes():
     assert np.array_equal(out8.float().numpy(), _bf16_np(y.astype(np.float32)))
 
 
+def test_bf16_pointwise_block_against_shifted_window_float64():
+    """ops/conv.py:67-81: the depthwise window as 25 shifted slices of the zero-padded image in float64 (no F.conv2d),
+    ReLU, BF16, then a float64 GEMM with C_out != C (a transposed weight cannot even multiply), bias, BF16. The oracle
+    accumulates in FP32, so the bar is one BF16 step of the result plus the FP32 error of the sums."""
+    torch.manual_seed(21)
+    b, c, h, w, n = 2, 32, 7, 9, 48
+    x = torch.randn(b, c, h, w).to(torch.bfloat16)
+    dw_w, dw_b = (torch.randn(25, c) * 0.3).to(torch.bfloat16), torch.randn(c).to(torch.bfloat16)
+    pw, pb = (torch.randn(n, c) * 0.2).to(torch.bfloat16), torch.randn(n).to(torch.bfloat16)
+    out = ref.depthwise5x5_relu_pointwise(x, dw_w, dw_b, pw, pb)
+    assert out.shape == (b, n, h, w) and out.is_contiguous(memory_format=torch.channels_last)
+    xp = F.pad(x.double(), (2, 2, 2, 2))
+    hidden = dw_b.double().view(1, c, 1, 1).expand(b, c, h, w).clone()
+    for ky in range(5):
+        for kx in range(5):
+            hidden += xp[:, :, ky:ky + h, kx:kx + w] * dw_w[ky * 5 + kx].double().view(1, c, 1, 1)
+    hidden = hidden.clamp_min(0).to(torch.bfloat16).double()
+    rows = hidden.permute(0, 2, 3, 1).reshape(-1, c)
+    exact = rows @ pw.double().t() + pb.double()
+    mag = rows.abs() @ pw.double().abs().t() + pb.double().abs()
+    got = out.permute(0, 2, 3, 1).reshape(-1, n).double()
+    assert ((got - exact).abs() <= exact.abs() * 2**-8 + mag * 2**-18).all()
+
+
 # -- golden fixtures ---------------------------------------------------------------------------------------------
 
 

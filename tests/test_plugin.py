@@ -41,7 +41,8 @@ class _StubOp:
 
 
 OP_NAMES = ("quantize_mxfp8", "quantize_int8", "gelu_quantize", "gelu_quantize_int8", "int8_conv2d", "mxfp8_conv2d",
-            "depthwise5x5_relu_mxfp8", "depthwise5x5_relu_int8", "depthwise5x5_relu_pointwise_mxfp8",
+            "depthwise5x5_relu_mxfp8", "depthwise5x5_relu_int8", "depthwise5x5_relu_pointwise",
+            "depthwise5x5_relu_pointwise_mxfp8",
             "depthwise5x5_relu_pointwise_int8", "im2col_gather", "int8_conv2d_maxpool", "int8_linear",
             "int8_linear_quantize", "mxfp8_scaled_mm", "mxfp8_linear", "mxfp8_gelu_mlp", "bias_relu_quantize_int8",
             "conv2d_small_cin_quantize_int8")
