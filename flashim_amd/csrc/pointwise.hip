@@ -14,7 +14,8 @@
 // Matrix unit: v_mfma_f32_16x16x32_bf16, A = 16 output channels of the weight, B = 16 pixels; lane l supplies row l % 16
 // of A and column l % 16 of B over the same 8 K values (K group l / 16), so any assignment of K groups inside the
 // instruction multiplies matching pairs. Lane l receives D[4 (l / 16) + i][l % 16]: 4 consecutive output channels of
-// pixel l % 16, one 8-byte store. The bias is the accumulator's initial value (-0 without bias: x + (-0) == x).
+// pixel l % 16, written to a wavefront-private LDS row; the block's 16 output rows, contiguous in memory, then leave as
+// 16-byte stores of consecutive lanes. The bias is the accumulator's initial value (-0 without bias: x + (-0) == x).
 #include "common.h"
 
 namespace fim {
@@ -31,6 +32,10 @@ __global__ __launch_bounds__(256) void pw_bf16_kernel(const uint16_t* __restrict
   constexpr int WROW = K + 8;  // BF16 elements per staged weight row
   __shared__ __align__(16) uint16_t sw[N * WROW];
   __shared__ float sb[N];
+  // per wavefront: its 16 pixels' outputs, rows of N BF16 padded by 16 bytes (the 4-lane groups of one row land in
+  // other banks than the next row's)
+  constexpr int SROW = 2 * N + 16;
+  __shared__ __align__(16) uint8_t stage[PW_WAVES][16 * SROW];
   for (int i = threadIdx.x; i < N * (K / 8); i += 256) {
     const int r = i / (K / 8), c = i % (K / 8);
     *reinterpret_cast<uint4*>(&sw[r * WROW + 8 * c]) = *reinterpret_cast<const uint4*>(&w[(int64_t)r * K + 8 * c]);
@@ -69,16 +74,29 @@ __global__ __launch_bounds__(256) void pw_bf16_kernel(const uint16_t* __restrict
         acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, cur[s], acc[nb], 0, 0, 0);
       }
     }
-    const int64_t row = blk * 16 + r16;
-    if (row < M) {
+    // outputs through LDS: lane l writes 4 channels of pixel l % 16, then the block (16 rows of 2 N bytes, contiguous
+    // in the output) leaves as 16-byte stores of consecutive lanes, whole lines per instruction
+    uint8_t* const st = stage[threadIdx.x >> 6];
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        uint2 v;
-        v.x = pack_bf16x2(acc[nb][0], acc[nb][1]);
-        v.y = pack_bf16x2(acc[nb][2], acc[nb][3]);
-        *reinterpret_cast<uint2*>(&out[row * N + 16 * nb + 4 * g]) = v;
+    for (int nb = 0; nb < NB; ++nb) {
+      uint2 v;
+      v.x = pack_bf16x2(acc[nb][0], acc[nb][1]);
+      v.y = pack_bf16x2(acc[nb][2], acc[nb][3]);
+      *reinterpret_cast<uint2*>(st + r16 * SROW + 2 * (16 * nb + 4 * g)) = v;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0) (vmcnt, expcnt untouched): this wavefront's LDS writes
+    constexpr int CPR = 2 * N / 16;       // 16-byte chunks per pixel row
+    const int64_t rows_left = M - blk * 16;
+#pragma unroll
+    for (int i = 0; i < (16 * CPR + 63) / 64; ++i) {
+      const int c = lane + 64 * i;
+      const int r = c / CPR, q = c % CPR;
+      if (c < 16 * CPR && r < rows_left) {
+        const uint4 v = *reinterpret_cast<const uint4*>(st + r * SROW + 16 * q);
+        *reinterpret_cast<uint4*>(reinterpret_cast<uint8_t*>(out) + ((blk * 16 + r) * N) * 2 + 16 * q) = v;
       }
     }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // the staged rows read before the next block overwrites them
 #pragma unroll
     for (int s = 0; s < KS; ++s) cur[s] = nxt[s];
   }
@@ -109,7 +127,7 @@ int fim_pointwise_bf16(const uint16_t* x, int64_t M, int64_t K, const uint16_t* 
                        uint16_t* out, hipStream_t stream) {
   if (x == nullptr || weight == nullptr || out == nullptr || M < 0 || K <= 0 || N <= 0) return FIM_ERR_INVALID;
   if (K % 32 != 0 || K > 128 || N % 16 != 0 || N > 128) return FIM_ERR_UNSUPPORTED;
-  if (((uintptr_t)x % 16) != 0 || ((uintptr_t)weight % 16) != 0 || ((uintptr_t)out % 8) != 0) return FIM_ERR_UNSUPPORTED;
+  if (((uintptr_t)x % 16) != 0 || ((uintptr_t)weight % 16) != 0 || ((uintptr_t)out % 16) != 0) return FIM_ERR_UNSUPPORTED;
   if (M == 0) return FIM_OK;
   const int64_t nblocks = cdiv(M, 16);
   // Enough waves to keep every CU streaming (8 workgroups of 4 waves per CU on 256 CUs), each wave several blocks.

@@ -205,8 +205,8 @@ int fim_depthwise5x5_relu_pointwise_mxfp8(const uint16_t* x, int64_t B, int64_t 
                                           int pw_bias_dtype, uint16_t* out, hipStream_t stream);
 
 /* The BF16 refiner block's pointwise GEMM: out[m, n] = bf16(sum_k x[m, k] * w[n, k] + bias[n]) with FP32 accumulation.
- * x BF16 [M, K] (16-byte aligned), weight BF16 [N, K] (16-byte aligned), bias FP32 [N] or NULL, out BF16 [M, N];
- * K in {32, 64, 96, 128}, N a multiple of 16 up to 128 (else 99). With fim_depthwise5x5 (act 0, out_mode 2) it
+ * x BF16 [M, K] (16-byte aligned), weight BF16 [N, K] (16-byte aligned), bias FP32 [N] or NULL, out BF16 [M, N]
+ * (16-byte aligned); K in {32, 64, 96, 128}, N a multiple of 16 up to 128 (else 99). With fim_depthwise5x5 (act 0, out_mode 2) it
  * replaces the fused BF16 block behind ops.depthwise5x5_relu_pointwise (flashim/ops/conv.py:67-84; the CUDA launcher
  * it stands for is launch_depthwise5x5_relu_pointwise, flashim/backends/cuda/conv.py:194-209). */
 int fim_pointwise_bf16(const uint16_t* x, int64_t M, int64_t K, const uint16_t* weight, int64_t N, const float* bias,
