@@ -36,6 +36,22 @@ CFG2_TRAFFIC_BYTES = int((6264.1 * 2.0 + 20000.0 * 1.0) * 1024)  # the op's one 
 # The config-4 block's algorithmic HBM bytes when fused (204.8 MB for 2 x 400 x 400 x 64: 10 bytes per
 # element); GBps_own_launches divides instead the bytes this library's own launches of the block must move once.
 CFG4_FUSED_BYTES = 204_800_000
+# Vector-ALU issue floor of the GELU-bearing kernels: SQ_INSTS_VALU per launch (wave instructions) from rocprofv3
+# --pmc runs (profiles/*.md), x 4 cycles per 64-lane instruction on a 16-lane SIMD / 1024 SIMDs / 2.4 GHz. These
+# kernels are bound by that floor before HBM or MFMA; re-measured by hand when a kernel changes.
+VALU_INSTS = {
+    "cfg2_mxfp8_1x1_gelu": 4.195e6,         # conv_igemm_wide_kernel (GELU epilogue)
+    "cfg3_mxfp8_3x3_bn_relu": 2.678e6,      # conv_patch_kernel
+    "cfg4_depthwise_gelu_mxfp8": 8.536e6,   # dw5x5_mfma_kernel<GELU, static MXFP8>
+}
+CLOCK_GHZ, SIMDS = 2.4, 1024
+
+
+def valu_floor_ms(name: str) -> float | None:
+    n = VALU_INSTS.get(name)
+    return None if n is None else n * 4 / SIMDS / (CLOCK_GHZ * 1e9) * 1e3
+
+
 DEV = "cuda"
 
 
@@ -237,8 +253,9 @@ def stem():
 
 def dwpw_block():
     """The depthwise-then-pointwise refiner blocks at the shape FlashIM times its fused kernels on (2 x 128 x 400 x 400,
-    flashim/backends/triton/conv.py:572-574): depthwise 5x5 + bias + ReLU -> dynamic MXFP8 / static INT8 -> 128 x 128
-    pointwise + bias -> BF16, as one kernel and as the two-launch composite. HBM bytes: BF16 in + BF16 out."""
+    flashim/backends/triton/conv.py:572-574): depthwise 5x5 + bias + ReLU -> BF16 / dynamic MXFP8 / static INT8 ->
+    128 x 128 pointwise + bias -> BF16; the quantized blocks also as one kernel and as the two-launch composite. HBM
+    bytes: BF16 in + BF16 out."""
     from flashim_amd import ops, quant
     from flashim_amd.backends.hip import conv as hip_conv
 
@@ -252,8 +269,11 @@ def dwpw_block():
                               quant.exponent_to_e8m0(pw.scale_exponent), pw_b)]
     i8 = [t.to(DEV) for t in (x, dw_w, dw_b, torch.randint(-127, 128, (c, c), dtype=torch.int8, generator=g),
                               torch.rand(c, generator=g) * 0.01 + 0.001, pw_b, torch.tensor(0.03))]
+    bf = [t.to(DEV) for t in (x, dw_w, dw_b.to(torch.bfloat16),
+                              (torch.randn(c, c, generator=g) * 0.1).to(torch.bfloat16), pw_b.to(torch.bfloat16))]
     nbytes = 2 * 400 * 400 * c * 2 * 2
     return {
+        "bf16_op": lambda: ops.depthwise5x5_relu_pointwise(*bf),
         "mxfp8_op": lambda: ops.depthwise5x5_relu_pointwise_mxfp8(*mx),
         "mxfp8_one_kernel": lambda: hip_conv.pointwise_mxfp8_fused(*mx),
         "mxfp8_composite": lambda: hip_conv.pointwise_mxfp8_composite(*mx),
@@ -419,6 +439,10 @@ def main() -> int:
                     "blocks": info["blocks"], "pixels_per_scale": info["pixels"],
                 }
 
+    for name, r in results.items():
+        floor = valu_floor_ms(name)
+        if floor is not None:
+            r.update({"valu_floor_ms": round(floor, 5), "valu_frac": round(floor / r["ms"], 4)})
     if only is not None:
         print(json.dumps({"workload": only, "results": results}))
         return 0
@@ -436,7 +460,9 @@ def main() -> int:
                    "M": 20000, "N": 512, "K": 512, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved_gbs / PEAK_HBM_GBS, 4), "traffic": CFG2_TRAFFIC_BYTES,
-                     "mfma_frac": round(value / PEAK_MX_TFLOPS, 4), "algorithmic_bytes": info["bytes"]},
+                     "mfma_frac": round(value / PEAK_MX_TFLOPS, 4), "algorithmic_bytes": info["bytes"],
+                     "valu_floor_ms": round(valu_floor_ms("cfg2_mxfp8_1x1_gelu"), 5),
+                     "valu_frac": round(valu_floor_ms("cfg2_mxfp8_1x1_gelu") / ms, 4)},
         "configs": results,
     }
     if not a.no_cpu:
