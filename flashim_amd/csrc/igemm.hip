@@ -1077,7 +1077,7 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
 
 // ---- Patch tiles -----------------------------------------------------------------------------------------------
 // Stride-1, dilation-1 3 x 3 convolutions with Cin == 128 (each of the 9 K steps is one tap's 128 channels).
-// Persistent workgroups of 8 wavefronts, one per CU, walk tiles of TH x TW (12 x 16) output pixels of one image x 64
+// Persistent workgroups of 8 wavefronts, one per CU, walk tiles of TH x TW (8 x 16) output pixels of one image x 64
 // output channels.
 // * The workgroup's 64 output channels of the weights (9 taps x 64 x 128 B = 72 KB) stay in LDS for all its tiles
 //   (tiles are dealt so a workgroup keeps one channel block), with their MX exponents packed into registers.
@@ -1476,8 +1476,9 @@ __global__ __launch_bounds__(512, 1) void conv_patch_kernel(const ConvArgs a) {
   }
 }
 
-// Patch tiles: 12 x 16 output pixels x 64 channels.
-constexpr int PATCH_TH = 12, PATCH_TW = 16;
+// Patch tiles: 8 x 16 output pixels x 64 channels (config 3: 1300 tiles, at most 6 per workgroup for 5.08 on average:
+// 18.98 us; 12 x 16 tiles, 884 of them, at most 4 for 3.45, 19.5 us; 4 x 16, 19.8 us).
+constexpr int PATCH_TH = 8, PATCH_TW = 16;
 
 static int64_t patch_grid(int64_t tiles, int64_t n_tiles) {
   // a multiple of 8 (XCDs) and of the channel-block count (each workgroup keeps one), at most one per CU
