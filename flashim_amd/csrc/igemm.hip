@@ -1812,6 +1812,218 @@ static int launch_pw(ConvArgs a, int ks, hipStream_t stream) {
   return launch_status();
 }
 
+// ---- Pointwise, whole K resident ---------------------------------------------------------------------------------
+// 1 x 1 stride-1 convolutions with Cin a multiple of 128 up to 512 and about one to two 160-pixel tiles per CU (config
+// 2: 125 x 4 tiles on 256 CUs), where every other kernel here runs each CU's work as one serial sequence of loads,
+// MFMAs and a long GELU epilogue. Persistent workgroups of 8 wavefronts, one per CU, keep one 128-channel block:
+// * the block's weights (128 x Cin bytes) and a tile's activations (160 x Cin bytes) are all in LDS at once (K steps
+//   side by side, [step][row][128 B] with the conv stages' slot swizzle), so the K loop has no barrier and no wait;
+// * after a tile's MFMAs, one barrier, then the next tile's activation loads (wave-wide `buffer_load ... lds`) are
+//   issued and run while this tile's epilogue keeps the VALU busy; the weights are loaded once.
+// Wavefront w takes 80 pixels (w % 2) x 32 channels (w / 2): 5 x 2 blocks of 16 x 16, 7 fragment reads per 10 MFMAs.
+constexpr int RES_MB = 5, RES_NB = 2, RES_WM = 2, RES_BM = RES_WM * RES_MB * 16, RES_BN = 4 * RES_NB * 16;
+
+template <int KIND, int OUT, int KS>
+__global__ __launch_bounds__(512, 1) void conv_1x1_resident_kernel(const ConvArgs a) {
+  constexpr int MB = RES_MB, NB = RES_NB, BM = RES_BM, BN = RES_BN;
+  constexpr int STAGE = (BM + BN) * KC;       // one K step: activation rows, then weight rows
+  constexpr int ACH = BM / 8, BCH = BN / 8;   // 1 KB chunks (8 rows x 128 B) per K step
+  constexpr int ALOADS = (KS * ACH + 7) / 8, BLOADS = (KS * BCH + 7) / 8;  // per wavefront
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[KS * STAGE];
+  __shared__ __attribute__((aligned(16))) float ep_scale[BN], ep_bias[BN], ep_osc[BN];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % RES_WM, wn = wave / RES_WM;
+  const int g = lane >> 4;
+
+  // tiles (m tile, channel block), dealt as in the pointwise kernel: XCD-aware, one channel block per workgroup
+  const int m_tiles = (a.M + BM - 1) / BM;
+  const int total = a.n_tiles * m_tiles;
+  const int stride = gridDim.x;
+  const int per_xcd = stride >> 3;
+  const int first = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (first >= total) return;
+  const int n0 = (first % a.n_tiles) * BN;
+
+  if (tid < BN) {
+    const int n = n0 + tid;
+    const bool nok = n < a.Cout;
+    ep_scale[tid] = (KIND == KIND_INT8 && nok) ? *a.a_scale * a.w_scale[n] : 1.0f;
+    float bias = -0.0f;
+    if (a.bias != nullptr && nok)
+      bias = a.bias_dtype == FIM_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(a.bias)[n])
+                                      : static_cast<const float*>(a.bias)[n];
+    ep_bias[tid] = bias;
+    ep_osc[tid] = (OUT == OUT_E4M3 && nok) ? exp2_int((int)a.out_expo[n >> 5]) : 1.0f;
+  }
+
+  const int x_nrec = __builtin_amdgcn_readfirstlane((int)((int64_t)a.M * a.Cin));
+  const int w_nrec = __builtin_amdgcn_readfirstlane(a.Cout * a.Cin);
+  constexpr uint32_t OOB = 0x80000000u;
+  // lane's row within a chunk and the global segment it fetches (slot lane % 8 holds segment (lane % 8) ^ ((r / 2) % 8))
+  const int crow = lane >> 3;
+
+  // all K steps of tile t's activation rows (rows past M read as zero)
+  auto load_a = [&](int t) __attribute__((always_inline)) {
+    const int m0 = (t / a.n_tiles) * BM;
+#pragma unroll
+    for (int i = 0; i < ALOADS; ++i) {
+      const int k = wave + 8 * i;
+      if (k < KS * ACH) {  // uniform
+        const int st = k / ACH, c = k % ACH;
+        const int r = 8 * c + crow;
+        const int seg = (lane & 7) ^ ((r >> 1) & 7);
+        const int m = m0 + r;
+        const uint32_t off = m < a.M ? (uint32_t)(m * a.Cin + st * KC + seg * 16) : OOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.x), (short)0, x_nrec, 0x00020000),
+            (lds_void_t*)(smem + st * STAGE + c * 1024), 16, off, 0, 0, 0);
+      }
+    }
+  };
+  // the block's weight rows, every K step (channels past Cout read as zero)
+#pragma unroll
+  for (int i = 0; i < BLOADS; ++i) {
+    const int k = wave + 8 * i;
+    if (k < KS * BCH) {
+      const int st = k / BCH, c = k % BCH;
+      const int r = BM + 8 * c + crow;  // LDS row
+      const int seg = (lane & 7) ^ ((r >> 1) & 7);
+      const int n = n0 + r - BM;
+      const uint32_t off = n < a.Cout ? (uint32_t)(n * a.Cin + st * KC + seg * 16) : OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), (short)0, w_nrec, 0x00020000),
+          (lds_void_t*)(smem + st * STAGE + (ACH + c) * 1024), 16, off, 0, 0, 0);
+    }
+  }
+  load_a(first);
+
+  // fragment offsets within a K step (the conv stages' layout: lo half at f, hi half at f ^ 64)
+  int fr_x[MB], fr_w[NB];
+#pragma unroll
+  for (int j = 0; j < MB; ++j) {
+    const int r = wm * (MB * 16) + j * 16 + (lane & 15);
+    fr_x[j] = r * KC + ((g ^ ((r >> 1) & 7)) << 4);
+  }
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int r = BM + wn * (NB * 16) + i * 16 + (lane & 15);
+    fr_w[i] = r * KC + ((g ^ ((r >> 1) & 7)) << 4);
+  }
+  // MXFP8 scales per K step: the lane's activation block 4 st + g and its weight rows' bytes of that block
+  int sx[KS], sw[KS][NB];
+  if constexpr (KIND == KIND_MX) {
+    const int cblocks = a.Cin >> 5;
+#pragma unroll
+    for (int st = 0; st < KS; ++st) {
+      sx[st] = (int)a.x_expo[4 * st + g] + 127;
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const int n = n0 + wn * (NB * 16) + i * 16 + (lane & 15);
+        sw[st][i] = (int)a.w_expo[(int64_t)(n < a.Cout ? n : 0) * cblocks + 4 * st + g] + 127;
+      }
+    }
+  }
+
+  vm_lds_barrier();  // weights and the first tile landed
+  for (int t = first; t < total; t += stride) {
+    v4i acc_i[NB][MB];
+    v4f acc_f[NB][MB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int j = 0; j < MB; ++j) {
+        acc_i[i][j] = v4i{0, 0, 0, 0};
+        acc_f[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+    for (int st = 0; st < KS; ++st) {
+      const uint8_t* cur = smem + st * STAGE;
+      v8i xf[MB], wf[NB];
+#pragma unroll
+      for (int j = 0; j < MB; ++j) {
+        const v4i lo = *reinterpret_cast<const v4i*>(cur + fr_x[j]);
+        const v4i hi = *reinterpret_cast<const v4i*>(cur + (fr_x[j] ^ 64));
+        xf[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const v4i lo = *reinterpret_cast<const v4i*>(cur + fr_w[i]);
+        const v4i hi = *reinterpret_cast<const v4i*>(cur + (fr_w[i] ^ 64));
+        wf[i] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+          if constexpr (KIND == KIND_INT8) {
+            acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_shufflevector(wf[i], wf[i], 0, 1, 2, 3),
+                                                                __builtin_shufflevector(xf[j], xf[j], 0, 1, 2, 3),
+                                                                acc_i[i][j], 0, 0, 0);
+            acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_shufflevector(wf[i], wf[i], 4, 5, 6, 7),
+                                                                __builtin_shufflevector(xf[j], xf[j], 4, 5, 6, 7),
+                                                                acc_i[i][j], 0, 0, 0);
+          } else {
+            acc_f[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[i], xf[j], acc_f[i][j], 0, 0, 0,
+                                                                           sw[st][i], 0, sx[st]);
+          }
+        }
+    }
+    // the accumulators pinned (else the MFMAs sink into the epilogue, past the barrier, with their operands live)
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int j = 0; j < MB; ++j) {
+        if constexpr (KIND == KIND_INT8)
+          asm volatile("" : "+v"(acc_i[i][j]));
+        else
+          asm volatile("" : "+v"(acc_f[i][j]));
+      }
+    lds_barrier();  // every wavefront has read this tile's activations
+    const int next = t + stride;
+    if (next < total) load_a(next);
+    conv_epilogue<KIND, OUT, 0, MB, NB>(a, acc_i, acc_f, (t / a.n_tiles) * BM + wm * (MB * 16), n0, wn * (NB * 16),
+                                        ep_scale, ep_bias, ep_osc);
+    if (next < total) vm_lds_barrier();  // the next tile's activations landed
+  }
+}
+
+// Whether the resident-K pointwise kernel applies: the pointwise kernel's shape conditions (1 x 1, stride 1, no
+// padding, Cin % 128 == 0 up to 512, 16-byte aligned operands and output) and at least one 160-pixel tile per CU.
+static int res_ks(const ConvArgs& a, int lw) {
+  if (lw != 16 || a.pool_out != nullptr || a.a_scale_rows != nullptr || a.x_swz != nullptr) return 0;
+  if (a.kh != 1 || a.kw != 1 || a.sh != 1 || a.sw != 1 || a.ph != 0 || a.pw != 0) return 0;
+  if (a.Cin % KC != 0 || a.Cin > 4 * KC || a.Cout < 128) return 0;
+  if ((int64_t)a.M * a.Cin >= (1LL << 31) - 16 || (int64_t)a.Cout * a.Cin >= (1LL << 31)) return 0;
+  if (cdiv((int64_t)a.M, RES_BM) * cdiv((int64_t)a.Cout, RES_BN) < device_cus()) return 0;
+  return a.Cin / KC;
+}
+
+template <int KIND, int OUT>
+static void launch_res_ks(const ConvArgs& a, int ks, dim3 grid, hipStream_t stream) {
+  switch (ks) {
+    case 1: conv_1x1_resident_kernel<KIND, OUT, 1><<<grid, dim3(512), 0, stream>>>(a); break;
+    case 2: conv_1x1_resident_kernel<KIND, OUT, 2><<<grid, dim3(512), 0, stream>>>(a); break;
+    case 3: conv_1x1_resident_kernel<KIND, OUT, 3><<<grid, dim3(512), 0, stream>>>(a); break;
+    default: conv_1x1_resident_kernel<KIND, OUT, 4><<<grid, dim3(512), 0, stream>>>(a); break;
+  }
+}
+
+template <int KIND>
+static int launch_res(ConvArgs a, int ks, hipStream_t stream) {
+  a.n_tiles = (int)cdiv(a.Cout, RES_BN);
+  const int64_t tiles = cdiv((int64_t)a.M, RES_BM) * a.n_tiles;
+  const dim3 grid((unsigned)patch_grid(tiles, a.n_tiles));
+  constexpr int QOUT = KIND == KIND_INT8 ? OUT_INT8 : OUT_E4M3;
+  if (a.out_mode == OUT_BF16)
+    launch_res_ks<KIND, OUT_BF16>(a, ks, grid, stream);
+  else
+    launch_res_ks<KIND, QOUT>(a, ks, grid, stream);
+  return launch_status();
+}
+
 template <int KIND, int WM>
 static void launch_wide(const ConvArgs& a, dim3 grid, hipStream_t stream) {
   constexpr int QOUT = KIND == KIND_INT8 ? OUT_INT8 : OUT_E4M3;
@@ -1936,6 +2148,7 @@ static int launch_conv(ConvArgs a, hipStream_t stream) {
   const bool fast_ok = a.out_mode == OUT_BF16 ? conv_fast_ok<OUT_BF16>(a) : conv_fast_ok<OUT_INT8>(a);
   if (patch_ok(a, lw, fast_ok)) return launch_patch<KIND>(a, stream);
   if (const int ks = pw_ks(a, lw, fast_ok)) return launch_pw<KIND>(a, ks, stream);
+  if (const int ks = res_ks(a, lw)) return launch_res<KIND>(a, ks, stream);
   if (const int wm = wide_wm(a, lw)) {
     a.n_tiles = (int)cdiv((int64_t)a.Cout, (8 / wm) * 64);
     a.m_tiles = (int)cdiv((int64_t)a.M, wm * 80);
