@@ -99,8 +99,9 @@ def test_config2_full_size():
 
 
 @pytest.mark.parametrize("cin", [512, 640])
-def test_config2_layer_wide_kernel_ring_tails(cin):
-    """The config-2 layer shape with four and five 128-byte K steps through the wide (three-stage) kernel."""
+def test_config2_layer_four_and_five_k_steps(cin):
+    """The config-2 layer shape with four 128-byte K steps (the whole-K pointwise kernel) and five (the wide
+    three-stage kernel, its ring of stages wrapping with a partial tail)."""
     g = torch.Generator().manual_seed(cin)
     x_bf16 = (torch.randn(2, 100, 100, cin, generator=g) * 2).to(torch.bfloat16)
     e = ref.calibrate_block32_exponent(x_bf16.float())

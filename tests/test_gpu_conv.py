@@ -475,8 +475,13 @@ def test_mxfp8_conv2d_patch_tiles(case):
 
 # (name, image (B, H, W), Cin, Cout): pointwise shapes (1 x 1, stride 1, Cin a multiple of 128 up to 512, Cout >= 128):
 # 1 to 4 K steps, a partial last tile of pixels, a partial channel block; the large ones run the register-operand
-# pointwise kernel, the small ones the one-round kernels
+# pointwise kernel, the "resident" ones (one to two 160-pixel tiles per CU on 256 CUs) the whole-K kernel, the small
+# ones the one-round kernels
 ROW_CASES = [
+    ("k1_n128_resident", (2, 150, 151), 128, 128),
+    ("k2_n144_resident", (2, 110, 111), 256, 144),
+    ("k3_n256_resident", (1, 150, 151), 384, 256),
+    ("k4_n512_resident", (2, 100, 101), 512, 512),
     ("k1_partial_tile", (1, 7, 13), 128, 128),
     ("k2_n144", (2, 9, 11), 256, 144),
     ("k3_n256", (1, 30, 31), 384, 256),
