@@ -60,7 +60,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--only", default=None, help="run one workload only (cfg1|cfg2|cfg3|cfg3q|dw|stem|dwpw|cfg4|cfg5int8|cfg5mxfp8|copy)"
+    p.add_argument("--only", default=None, help="run one workload only (cfg1|cfg2|cfg3|cfg3q|dw|stem|dwpw|cfg4|cfg5int8|cfg5mxfp8|copy|peaks)"
                                                   " and print its line (profiling runs)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-stack", action="store_true", help="skip configs 4 and 5")
@@ -289,6 +289,27 @@ def copy_calibration():
     return lambda: dst.copy_(src), src.numel()
 
 
+def measured_peaks(steps: int, warmup: int) -> dict:
+    """The box's own peaks, beside the datasheet ones: MFMA throughput from the register-only microbenchmark
+    (``fim_test_mfma_peak``: 8 wavefronts per SIMD, back-to-back independent 16 x 16 MFMAs) and HBM bandwidth from a
+    plain 64 MiB device copy (read + write)."""
+    from flashim_amd import _lib
+
+    blocks = 8 * torch.cuda.get_device_properties(0).multi_processor_count
+    out = torch.empty(blocks * 256, device=DEV, dtype=torch.float32)
+    iters = 400
+    res = {}
+    for kind, name, ops_each in ((0, "mfma_mxfp8_TFLOPs", 65536), (1, "mfma_int8_TOPs", 32768)):
+        fn = lambda k=kind: _lib.call("fim_test_mfma_peak", k, blocks, iters, out.data_ptr(),  # noqa: E731
+                                      _lib.stream_of(out), what="mfma peak")
+        ms = time_graph(fn, max(steps // 5, 3), 2, per_graph=1)
+        res[name] = round(blocks * 4 * iters * 8 * ops_each / (ms * 1e-3) / 1e12, 1)
+    fn, nbytes = copy_calibration()
+    ms = time_graph(fn, steps, warmup)
+    res["copy_GBps"] = round(2 * nbytes / (ms * 1e-3) / 1e9, 1)
+    return res
+
+
 # -- CPU baseline (oracle) ---------------------------------------------------------------------------------------
 
 
@@ -351,6 +372,10 @@ def main() -> int:
         fn, nbytes = copy_calibration()
         ms = time_graph(fn, steps, warmup)
         print(json.dumps({"workload": "copy", "bytes": nbytes, "ms": ms, "GBps": 2 * nbytes / ms / 1e6}))
+        return 0
+
+    if a.only == "peaks":
+        print(json.dumps({"workload": "peaks", "results": measured_peaks(steps, warmup)}))
         return 0
 
     results = {}
@@ -465,6 +490,10 @@ def main() -> int:
                      "valu_frac": round(valu_floor_ms("cfg2_mxfp8_1x1_gelu") / ms, 4)},
         "configs": results,
     }
+    peaks = measured_peaks(steps, warmup)
+    line["measured_peaks"] = peaks
+    line["roofline"]["frac_of_measured_copy"] = round(achieved_gbs / peaks["copy_GBps"], 4)
+    line["roofline"]["mfma_frac_of_measured"] = round(value / peaks["mfma_mxfp8_TFLOPs"], 4)
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline_cfg2(c2_args)
         line["cpu_baseline_cfg1"] = cpu_baseline_cfg1(cfg1()[2])

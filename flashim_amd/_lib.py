@@ -62,6 +62,7 @@ SIGNATURES: dict[str, list] = {
                                               _vp],
     "fim_test_e4m3": [_vp, _i64, _vp, _vp],
     "fim_test_mx_exponent": [_vp, _i64, _vp, _vp],
+    "fim_test_mfma_peak": [_i32, _i64, _i32, _vp, _vp],
     "fim_test_bf16": [_vp, _i64, _vp, _vp],
     "fim_test_gelu": [_vp, _i64, _vp, _vp],
 }

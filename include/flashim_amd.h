@@ -228,6 +228,12 @@ int fim_test_gelu(const uint16_t* x, int64_t n, uint16_t* out, hipStream_t strea
 /* MX exponents of n FP32 amax values with the device rule (quant/formats/mx.py:22-26). */
 int fim_test_mx_exponent(const float* amax, int64_t n, int8_t* out, hipStream_t stream);
 
+/* MFMA throughput microbenchmark (no counterpart in the reference; the measured peak the roofline fractions are also
+ * quoted against): `blocks` workgroups of 256 threads, each wavefront `iters` rounds of 8 independent 16 x 16 MFMAs on
+ * register operands. kind 0: scaled MXFP8 16x16x128 (65536 FLOP each), 1: INT8 16x16x64 (32768 OP each). out: FP32
+ * [blocks * 256], one sum per thread. */
+int fim_test_mfma_peak(int kind, int64_t blocks, int iters, float* out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -84,3 +84,13 @@ def test_gelu_within_one_bf16_rounding_of_torch_on_every_bf16_input():
     diff = (got - want).abs()[ok]
     assert (diff <= want.abs()[ok] * 2**-7 + 2**-12).all()
     assert (got[ok] != want[ok]).float().mean() < 0.02
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", [0, 1])
+def test_mfma_peak_hook_runs(kind):
+    """The MFMA microbenchmark the bench quotes its measured peaks from: it runs and every thread's sum is finite."""
+    out = torch.empty(4 * 256, device="cuda", dtype=torch.float32)
+    _lib.call("fim_test_mfma_peak", kind, 4, 10, out.data_ptr(), _lib.stream_of(out))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
