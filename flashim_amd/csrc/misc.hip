@@ -29,7 +29,8 @@ __global__ void test_mx_exponent_kernel(const float* amax, int64_t n, int8_t* ou
 
 // MFMA throughput microbenchmark: every wavefront runs `iters` rounds of 8 independent 16 x 16 MFMAs on register
 // operands (no memory traffic in the loop; the operands depend on the lane, the sum is written out so nothing is
-// dropped). kind 0: v_mfma_scale_f32_16x16x128_f8f6f4 (MXFP8, 65536 FLOP each), 1: v_mfma_i32_16x16x64_i8 (32768 OP).
+// dropped). kind 0: v_mfma_scale_f32_16x16x128_f8f6f4 (MXFP8, 65536 FLOP each), 1: v_mfma_i32_16x16x64_i8 (32768 OP),
+// 2: v_mfma_i32_32x32x32_i8 (65536 OP).
 template <int KIND>
 __global__ __launch_bounds__(256) void mfma_peak_kernel(int iters, float* out) {
   const int lane = threadIdx.x & 63;
@@ -41,26 +42,31 @@ __global__ __launch_bounds__(256) void mfma_peak_kernel(int iters, float* out) {
   }
   v4f accf[8];
   v4i acci[8];
+  v16i acc32[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     accf[j] = v4f{0.f, 0.f, 0.f, 0.f};
     acci[j] = v4i{0, 0, 0, 0};
+    acc32[j] = v16i{};
   }
   for (int it = 0; it < iters; ++it) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if constexpr (KIND == 0)
         accf[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, accf[j], 0, 0, 0, 127, 0, 127);
-      else
+      else if constexpr (KIND == 1)
         acci[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_shufflevector(a, a, 0, 1, 2, 3),
                                                         __builtin_shufflevector(b, b, 0, 1, 2, 3), acci[j], 0, 0, 0);
+      else
+        acc32[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_shufflevector(a, a, 0, 1, 2, 3),
+                                                         __builtin_shufflevector(b, b, 0, 1, 2, 3), acc32[j], 0, 0, 0);
     }
   }
   float sum = 0.f;
 #pragma unroll
   for (int j = 0; j < 8; ++j)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) sum += KIND == 0 ? accf[j][e] : (float)acci[j][e];
+    for (int e = 0; e < 4; ++e) sum += KIND == 0 ? accf[j][e] : KIND == 1 ? (float)acci[j][e] : (float)acc32[j][e];
   out[blockIdx.x * blockDim.x + threadIdx.x] = sum;
 }
 
@@ -101,12 +107,14 @@ int fim_test_mx_exponent(const float* amax, int64_t n, int8_t* out, hipStream_t 
 }
 
 int fim_test_mfma_peak(int kind, int64_t blocks, int iters, float* out, hipStream_t stream) {
-  if (out == nullptr || blocks <= 0 || blocks > (1 << 20) || iters <= 0 || (kind != 0 && kind != 1))
+  if (out == nullptr || blocks <= 0 || blocks > (1 << 20) || iters <= 0 || kind < 0 || kind > 2)
     return FIM_ERR_INVALID;
   if (kind == 0)
     mfma_peak_kernel<0><<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(iters, out);
-  else
+  else if (kind == 1)
     mfma_peak_kernel<1><<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(iters, out);
+  else
+    mfma_peak_kernel<2><<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(iters, out);
   return launch_status();
 }
 

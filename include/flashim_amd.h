@@ -230,7 +230,8 @@ int fim_test_mx_exponent(const float* amax, int64_t n, int8_t* out, hipStream_t 
 
 /* MFMA throughput microbenchmark (no counterpart in the reference; the measured peak the roofline fractions are also
  * quoted against): `blocks` workgroups of 256 threads, each wavefront `iters` rounds of 8 independent 16 x 16 MFMAs on
- * register operands. kind 0: scaled MXFP8 16x16x128 (65536 FLOP each), 1: INT8 16x16x64 (32768 OP each). out: FP32
+ * register operands. kind 0: scaled MXFP8 16x16x128 (65536 FLOP each), 1: INT8 16x16x64 (32768 OP each), 2: INT8
+ * 32x32x32 (65536 OP each). out: FP32
  * [blocks * 256], one sum per thread. */
 int fim_test_mfma_peak(int kind, int64_t blocks, int iters, float* out, hipStream_t stream);
 

@@ -87,7 +87,7 @@ def test_gelu_within_one_bf16_rounding_of_torch_on_every_bf16_input():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("kind", [0, 1, 2])
 def test_mfma_peak_hook_runs(kind):
     """The MFMA microbenchmark the bench quotes its measured peaks from: it runs and every thread's sum is finite."""
     out = torch.empty(4 * 256, device="cuda", dtype=torch.float32)
