@@ -53,3 +53,25 @@ def test_stack_runs_and_is_deterministic():
     first = blocks.run_stack(scales[:1])
     again = blocks.run_stack(scales[:1])
     assert all(torch.equal(a, b) for a, b in zip(first, again))
+
+
+def test_stack_two_streams_matches_serial():
+    """The directions on two streams give the serial stack's bits, eagerly and in every replay of a captured graph
+    (replayed several times with eager work and synchronizations in between)."""
+    scales = blocks.build_stack("mxfp8", DEV)[:2]  # the two coarsest scales
+    side = torch.cuda.Stream()
+    want = blocks.run_stack(scales)
+    got = blocks.run_stack(scales, side)
+    torch.cuda.synchronize()
+    assert len(got) == len(want) and all(torch.equal(a, b) for a, b in zip(got, want))
+    graph = torch.cuda.CUDAGraph()
+    blocks.run_stack(scales, side)  # warm-up outside the capture
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        captured = blocks.run_stack(scales, side)
+    for _ in range(3):
+        eager = blocks.run_stack(scales)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(captured, eager))
