@@ -191,6 +191,9 @@ def run_stack(scales, side: torch.cuda.Stream | None = None) -> list[Tensor]:
         first, *rest = inputs
         with torch.cuda.stream(side):
             others = [chain(x, blocks) for x in rest]
+        if not torch.cuda.is_current_stream_capturing():
+            for o in others:  # read on the current stream: not reused by the side stream's allocations before that
+                o.record_stream(current)
         outs += [chain(first, blocks), *others]
     current.wait_stream(side)  # every output is complete on the current stream
     return outs
