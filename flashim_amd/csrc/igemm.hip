@@ -270,10 +270,12 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
           __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rsrc, (int)off, 0, 0);
       } else {
         uint32_t pk;
-        if (OUT == OUT_INT8) {
-          pk = 0;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) pk |= (uint32_t)(uint8_t)quantize_int8_fast(v[e], out_scale, out_inv) << (8 * e);
+        if (OUT == OUT_INT8) {  // the block's 4 values share one near-tie test (one wave-uniform branch)
+          const float vq[4] = {v[0], v[1], v[2], v[3]};
+          int qi[4];
+          quantize_int8_fast_n<4>(vq, out_scale, out_inv, qi);
+          pk = (uint32_t)(qi[0] & 0xff) | ((uint32_t)(qi[1] & 0xff) << 8) | ((uint32_t)(qi[2] & 0xff) << 16) |
+               ((uint32_t)qi[3] << 24);
         } else {
           pk = e4m3x4_of_bf16(v[0], v[1], v[2], v[3], osc[i], 448.0f * osc[i]);  // rounds to BF16 first
         }
