@@ -301,7 +301,7 @@ def measured_peaks(steps: int, warmup: int) -> dict:
     res = {}
     for kind, name, ops_each in ((0, "mfma_mxfp8_TFLOPs", 65536), (1, "mfma_int8_TOPs", 32768),
                                  (2, "mfma_int8_32x32x32_TOPs", 65536)):
-        fn = lambda k=kind: _lib.call("fim_test_mfma_peak", k, blocks, iters, out.data_ptr(),  # noqa: E731
+        fn = lambda k=kind: _lib.probe_call("fim_test_mfma_peak", k, blocks, iters, out.data_ptr(),  # noqa: E731
                                       _lib.stream_of(out), what="mfma peak")
         ms = time_graph(fn, max(steps // 5, 3), 2, per_graph=1)
         res[name] = round(blocks * 4 * iters * 8 * ops_each / (ms * 1e-3) / 1e12, 1)

@@ -1,5 +1,6 @@
 """Ahead-of-time build of the HIP library (``libflashim_amd.so``, gfx950) and of the host build of its scalar numerics
-(``libfim_host.so``, used by the CPU tests). The libraries are built in-tree so they travel with the source tree; the
+(``libfim_host.so``, used by the CPU tests), and the device probes the tests and the bench use
+(``libflashim_amd_probe.so``: numerics hooks and an MFMA microbenchmark, kept out of the product library). The libraries are built in-tree so they travel with the source tree; the
 ctypes loader in :mod:`flashim_amd._lib` only loads what is built and never compiles at import time.
 
 Flags: ``-ffp-contract=off`` keeps the epilogues' separate multiply and add roundings (the reference's order) unless a
@@ -19,7 +20,9 @@ CSRC = PACKAGE / "csrc"
 BUILD = PACKAGE / "_build"
 LIBRARY = PACKAGE / "libflashim_amd.so"
 HOST_LIBRARY = PACKAGE / "libfim_host.so"
-DEVICE_SOURCES = ("quantize.hip", "igemm.hip", "depthwise.hip", "dwpw.hip", "mlp.hip", "stem.hip", "pointwise.hip", "misc.hip")
+DEVICE_SOURCES = ("quantize.hip", "igemm.hip", "depthwise.hip", "dwpw.hip", "mlp.hip", "stem.hip", "pointwise.hip", "version.hip")
+PROBE_LIBRARY = PACKAGE / "libflashim_amd_probe.so"
+PROBE_SOURCES = ("probe.hip",)
 ARCH = os.environ.get("FLASHIM_AMD_ARCH", "gfx950")
 HIP_FLAGS = (
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract=off", "-munsafe-fp-atomics",
@@ -44,13 +47,16 @@ def build(jobs: int = 4) -> Path:
     """Compile every HIP source for gfx950 and link ``libflashim_amd.so``; build ``libfim_host.so``. Always rebuilds."""
     BUILD.mkdir(exist_ok=True)
     compiler = hipcc()
-    objects = [BUILD / (name.rsplit(".", 1)[0] + ".o") for name in DEVICE_SOURCES]
-    commands = [[compiler, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)] for src, obj in zip(DEVICE_SOURCES, objects)]
+    sources = DEVICE_SOURCES + PROBE_SOURCES
+    objects = {src: BUILD / (src.rsplit(".", 1)[0] + ".o") for src in sources}
+    commands = [[compiler, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(objects[src])] for src in sources]
     with ThreadPoolExecutor(max_workers=jobs) as pool:
         list(pool.map(_run, commands))
-    temporary = LIBRARY.with_suffix(f".{os.getpid()}.tmp")
-    _run([compiler, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objects), "-o", str(temporary)])
-    temporary.replace(LIBRARY)
+    for library, srcs in ((LIBRARY, DEVICE_SOURCES), (PROBE_LIBRARY, PROBE_SOURCES)):
+        temporary = library.with_suffix(f".{os.getpid()}.tmp")
+        _run([compiler, "-shared", "-fPIC", f"--offload-arch={ARCH}", *(str(objects[s]) for s in srcs),
+              "-o", str(temporary)])
+        temporary.replace(library)
     host_tmp = HOST_LIBRARY.with_suffix(f".{os.getpid()}.tmp")
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", str(CSRC / "numerics_host.cpp"), "-o", str(host_tmp)])
     host_tmp.replace(HOST_LIBRARY)

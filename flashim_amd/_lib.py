@@ -14,7 +14,7 @@ from pathlib import Path
 
 import torch
 
-from flashim_amd._build import HOST_LIBRARY, LIBRARY
+from flashim_amd._build import HOST_LIBRARY, LIBRARY, PROBE_LIBRARY
 
 FIM_ERR_INVALID = 98
 FIM_ERR_UNSUPPORTED = 99
@@ -28,8 +28,9 @@ SIGNATURES: dict[str, list] = {
     "fim_version": [],
     "fim_quantize_int8": [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp],
     "fim_quantize_mxfp8": [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp],
-    "fim_gelu_quantize_mxfp8": [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp],
-    "fim_gelu_quantize_int8": [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp],
+    "fim_gelu_quantize_mxfp8": [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _i64,
+                                _vp],
+    "fim_gelu_quantize_int8": [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp],
     "fim_quantize_mxfp8_dynamic": [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp],
     "fim_quantize_int8_rows": [_vp, _i32, _i64, _i64, _i64, _i32, _vp, _vp, _vp],
     "fim_calibrate_block32": [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp],
@@ -60,6 +61,10 @@ SIGNATURES: dict[str, list] = {
     "fim_pointwise_bf16": [_vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp],
     "fim_depthwise5x5_relu_pointwise_mxfp8": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _vp,
                                               _vp],
+}
+
+# the probe library (csrc/probe.h): test and measurement hooks, not part of the product ABI
+PROBE_SIGNATURES: dict[str, list] = {
     "fim_test_e4m3": [_vp, _i64, _vp, _vp],
     "fim_test_mx_exponent": [_vp, _i64, _vp, _vp],
     "fim_test_mfma_peak": [_i32, _i64, _i32, _vp, _vp],
@@ -76,6 +81,7 @@ class UnsupportedShape(RuntimeError):
 
 _lock = threading.Lock()
 _library: ctypes.CDLL | None = None
+_probe: ctypes.CDLL | None = None
 
 
 def library_path() -> Path:
@@ -100,6 +106,26 @@ def load() -> ctypes.CDLL:
                 fn.restype = ctypes.c_int
             _library = lib
     return _library
+
+
+def load_probe() -> ctypes.CDLL:
+    """The device probe library (tests and the bench's peak measurement only)."""
+    global _probe
+    with _lock:
+        if _probe is None:
+            if not PROBE_LIBRARY.is_file():
+                raise RuntimeError(f"{PROBE_LIBRARY} missing: build with `python -m flashim_amd._build`")
+            lib = ctypes.CDLL(str(PROBE_LIBRARY))
+            for name, argtypes in PROBE_SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.argtypes = argtypes
+                fn.restype = ctypes.c_int
+            _probe = lib
+    return _probe
+
+
+def probe_call(name: str, *args, what: str | None = None) -> None:
+    check(getattr(load_probe(), name)(*args), what or name)
 
 
 def available() -> bool:

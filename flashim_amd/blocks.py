@@ -176,7 +176,9 @@ def run_stack(scales, side: torch.cuda.Stream | None = None) -> list[Tensor]:
     """Every scale's blocks over each of its inputs; ``[scale 0 image A, scale 0 image B, scale 1 image A, ...]``.
     With ``side``, the second input of every scale (the other matching direction, independent of the first) runs on
     that stream concurrently with the first on the current stream: the same launches, so the same bits, but the
-    coarse scales' small launches overlap instead of each leaving most of the GPU idle."""
+    coarse scales' small launches overlap instead of each leaving most of the GPU idle. Eagerly, every tensor that
+    crosses streams is recorded on the stream that reads it; under graph capture the capture's private pool keeps
+    them alive for the graph's lifetime."""
     def chain(x, blocks):
         for block in blocks:
             x = block(x)
@@ -194,6 +196,8 @@ def run_stack(scales, side: torch.cuda.Stream | None = None) -> list[Tensor]:
         if not torch.cuda.is_current_stream_capturing():
             for o in others:  # read on the current stream: not reused by the side stream's allocations before that
                 o.record_stream(current)
+            for x in rest:  # read on the side stream: a caller freeing an input early cannot hand it to new work
+                x.record_stream(side)
         outs += [chain(first, blocks), *others]
     current.wait_stream(side)  # every output is complete on the current stream
     return outs

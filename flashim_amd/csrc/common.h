@@ -60,26 +60,15 @@ __device__ __forceinline__ float load_elem<FIM_F16>(const void* p, int64_t i) {
 // Hardware FP32 -> E4M3 (gfx950 v_cvt_pk_fp8_f32 is OCP E4M3, round to nearest even). The GPU tests check it
 // byte for byte against the software encoder in numerics.h over every BF16 value and random FP32 values.
 __device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float d) {
-#ifdef FIM_SOFTWARE_E4M3
-  return (uint32_t)f32_to_e4m3_sw(a) | ((uint32_t)f32_to_e4m3_sw(b) << 8) | ((uint32_t)f32_to_e4m3_sw(c) << 16) |
-         ((uint32_t)f32_to_e4m3_sw(d) << 24);
-#else
   int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
   int both = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
   return (uint32_t)both;
-#endif
 }
 
 // E4M3 codes of BF16(a..d) * 2^-e for values already within +-448 * 2^e (scale = 2^e): the pack rounds to BF16 and
 // v_cvt_scalef32_pk_fp8_bf16 divides by the scale and converts (RNE). Out-of-range values become NaN codes (the
 // conversion does not saturate), so callers clamp first.
 __device__ __forceinline__ uint32_t e4m3x4_of_bf16_inrange(float a, float b, float c, float d, float scale) {
-#ifdef FIM_SOFTWARE_E4M3
-  round_bf16x2(a, b);
-  round_bf16x2(c, d);
-  const float inv = 1.0f / scale;  // exact: a power of two
-  return pack_e4m3x4(a * inv, b * inv, c * inv, d * inv);
-#else
   typedef short v2s_t __attribute__((ext_vector_type(2)));
   typedef __bf16 v2bf_t __attribute__((ext_vector_type(2)));
   const v2s_t lo = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(v2s_t{0, 0}, __builtin_bit_cast(v2bf_t, pack_bf16x2(a, b)),
@@ -87,7 +76,6 @@ __device__ __forceinline__ uint32_t e4m3x4_of_bf16_inrange(float a, float b, flo
   const v2s_t both = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(lo, __builtin_bit_cast(v2bf_t, pack_bf16x2(c, d)),
                                                                scale, true);
   return __builtin_bit_cast(uint32_t, both);
-#endif
 }
 
 // E4M3 codes of BF16(a..d) * 2^-e, clamped to +-448: the BF16 rounding then static MXFP8 quantize of the references
@@ -105,11 +93,7 @@ __device__ __forceinline__ uint32_t e4m3x4_of_bf16(float a, float b, float c, fl
 }
 
 __device__ __forceinline__ uint8_t e4m3(float a) {
-#ifdef FIM_SOFTWARE_E4M3
-  return f32_to_e4m3_sw(a);
-#else
   return (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(a, a, 0, false) & 0xff);
-#endif
 }
 
 // GELU, erf form: 0.5 x erfc(-x / sqrt 2) = max(x, 0) - |x| E with E = erfc(|x| / sqrt 2) / 2 (x >= 0: x - x E;
@@ -138,6 +122,18 @@ __device__ __forceinline__ float gelu_erf(float x) {
   p = fmaf(p, u, -41.367184f);
   p = fmaf(p, u, -9.062012672f);  // the fit's constant -8.062 minus 1: the factor 1/2
   return fmaf(-fabsf(x), __builtin_amdgcn_exp2f(p), __builtin_elementwise_maximum(x, -0.0f));
+}
+
+// GELU, tanh form (F.gelu(approximate="tanh")): 0.5 x (1 + tanh(y)), y = sqrt(2 / pi) (x + 0.044715 x^3), written
+// as x / (1 + e^(-2 y)) (1 + tanh y = 2 / (1 + e^(-2 y))): one v_exp_f32 and a correctly rounded division, no
+// cancellation in the negative tail (torch's 1 + tanh loses the low bits there; the two agree within |x| 2^-23 in
+// absolute terms). Limits: e -> inf gives x / inf = -0 for large negative x (torch: 0.5 x (1 - 1) = -0), e -> 0 gives
+// x; GELU(+-0) = +-0 and NaN stays NaN.
+__device__ __forceinline__ float gelu_tanh(float x) {
+  constexpr float kTwoK = 2.0f * 0.79788456080286535588f * 1.44269504088896340736f;  // 2 sqrt(2/pi) log2(e)
+  const float x2 = x * x;
+  const float t = -kTwoK * fmaf(0.044715f * x2, x, x);
+  return __fdiv_rn(x, 1.0f + __builtin_amdgcn_exp2f(t));
 }
 
 // gelu_erf over N independent values, written step by step (each Horner step over all N values before the next), so

@@ -1,5 +1,9 @@
-// Library version and the device test hooks declared in include/flashim_amd.h.
+// Device probes for the tests and the bench, built as their own library (libflashim_amd_probe.so) and kept out of
+// the product library and its public header: the kernels' numerics helpers evaluated element by element (checked
+// against torch on the GPU), and an MFMA throughput microbenchmark (the measured peaks the roofline fractions are also
+// quoted against). Declarations: probe.h.
 #include "common.h"
+#include "probe.h"
 
 namespace fim {
 
@@ -75,8 +79,6 @@ __global__ __launch_bounds__(256) void mfma_peak_kernel(int iters, float* out) {
 using namespace fim;
 
 extern "C" {
-
-int fim_version(void) { return 100; }
 
 int fim_test_e4m3(const float* x, int64_t n, uint8_t* out, hipStream_t stream) {
   if (x == nullptr || out == nullptr || n < 0) return FIM_ERR_INVALID;

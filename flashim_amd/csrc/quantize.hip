@@ -28,7 +28,8 @@ struct Geometry4 {
 
 // MODE_INT8: round(x * cs[c] / scale) (IEEE division); MODE_MX: clamp(x / 2^e[c/32], +-448) -> E4M3 (zero padding).
 // gelu != 0 first applies GELU in the input's dtype (the gelu_quantize producers, flashim/ops/quantize.py:63-74,
-// 128-131): x (+ in_bias[c] in FP32) -> erf GELU in FP32 -> rounded to the dtype code `rnd` (FP32: unrounded).
+// 128-131): x (+ in_bias[c] in FP32) -> GELU (erf or tanh form) in FP32 -> rounded to the dtype code `rnd` (FP32:
+// unrounded).
 enum { MODE_INT8 = 0, MODE_MX = 1 };
 
 template <int MODE>
@@ -37,14 +38,14 @@ struct Quantizer {
   float inv;              // INT8 1 / scale
   const float* cs;        // INT8 optional per-channel pre-multiplier (SmoothQuant's 1/s)
   const int8_t* expo;     // MX static exponents [Cpad / 32]
-  int gelu;               // GELU first (uniform)
+  int gelu;               // GELU first (uniform): 0 none, 1 erf form, 2 tanh form
   int rnd;                // dtype code the GELU result is rounded to
   const float* in_bias;   // GELU's optional FP32 input bias [C]
 
   __device__ __forceinline__ uint8_t operator()(float v, int64_t c) const {
     if (gelu) {
       if (in_bias != nullptr) v = __fadd_rn(v, in_bias[c]);
-      v = gelu_erf(v);
+      v = gelu == 2 ? gelu_tanh(v) : gelu_erf(v);
       if (rnd == FIM_BF16) v = round_bf16(v);
       else if (rnd == FIM_F16) v = (float)(_Float16)v;
     }
@@ -489,20 +490,23 @@ int fim_quantize_mxfp8(const void* x, int dtype, int64_t B, int64_t H, int64_t W
 }
 
 int fim_gelu_quantize_mxfp8(const void* x, int dtype, int64_t B, int64_t H, int64_t W, int64_t C, int64_t sb,
-                            int64_t sh, int64_t sw, int64_t sc, const float* input_bias, const int8_t* exponent,
-                            uint8_t* out, int64_t Cpad, hipStream_t stream) {
+                            int64_t sh, int64_t sw, int64_t sc, int approximate, const float* input_bias,
+                            const int8_t* exponent, uint8_t* out, int64_t Cpad, hipStream_t stream) {
   if (x == nullptr || exponent == nullptr || out == nullptr || B < 0 || H < 0 || W < 0 || C < 0) return FIM_ERR_INVALID;
+  if (approximate != 0 && approximate != 1) return FIM_ERR_INVALID;
   if (Cpad % 32 != 0 || Cpad < C || Cpad - C >= 32) return FIM_ERR_INVALID;
   Geometry4 g{B, H, W, C, sb, sh, sw, sc};
-  Quantizer<MODE_MX> qz{0.0f, 1.0f, nullptr, exponent, 1, dtype, input_bias};
+  Quantizer<MODE_MX> qz{0.0f, 1.0f, nullptr, exponent, 1 + approximate, dtype, input_bias};
   return dispatch_quantize<MODE_MX>(x, dtype, g, qz, nullptr, out, Cpad, stream);
 }
 
 int fim_gelu_quantize_int8(const void* x, int dtype, int64_t B, int64_t H, int64_t W, int64_t C, int64_t sb,
-                           int64_t sh, int64_t sw, int64_t sc, const float* scale, int8_t* out, hipStream_t stream) {
+                           int64_t sh, int64_t sw, int64_t sc, int approximate, const float* scale, int8_t* out,
+                           hipStream_t stream) {
   if (x == nullptr || scale == nullptr || out == nullptr || B < 0 || H < 0 || W < 0 || C < 0) return FIM_ERR_INVALID;
+  if (approximate != 0 && approximate != 1) return FIM_ERR_INVALID;
   Geometry4 g{B, H, W, C, sb, sh, sw, sc};
-  Quantizer<MODE_INT8> qz{0.0f, 1.0f, nullptr, nullptr, 1, dtype, nullptr};
+  Quantizer<MODE_INT8> qz{0.0f, 1.0f, nullptr, nullptr, 1 + approximate, dtype, nullptr};
   return dispatch_quantize<MODE_INT8>(x, dtype, g, qz, scale, reinterpret_cast<uint8_t*>(out), C, stream);
 }
 

@@ -3,7 +3,7 @@
 ``FLASHIM_OPS`` override grammar) so code written against ``flashim.ops`` runs unchanged on ``flashim_amd.ops``.
 
 The table is built for a backend that has no fallback. An op here holds only HIP impls; a call picks the first impl,
-in (priority, registration) order, whose device and features match the arguments' platform and whose ``accepts``
+in (priority, narrowest device spec, registration) order, whose device and features match the arguments' platform and whose ``accepts``
 (on the trailing weight operands) and ``when`` (on all arguments) predicates pass. When none does, the call raises
 ``NotImplementedError`` with every impl's reason: this package never computes a result anywhere but on its kernels.
 Inside FlashIM (:mod:`flashim_amd.plugin`) the same impls are registered on FlashIM's own ops, whose torch
@@ -50,6 +50,16 @@ class DeviceSpec:
         lo_ok = self.min_capability is None or (cap is not None and cap >= self.min_capability)
         hi_ok = self.max_capability is None or (cap is not None and cap <= self.max_capability)
         return lo_ok and hi_ok
+
+    @property
+    def span(self) -> float:
+        """How many capability versions the spec covers (major * 100 + minor, open ends at 0.0 and 99.99; ``"*"`` is
+        unbounded). Among impls of equal priority the narrower spec, the more specialized impl, is tried first."""
+        if self.type == "*":
+            return float("inf")
+        lo = self.min_capability or (0, 0)
+        hi = self.max_capability or (99, 99)
+        return float((hi[0] * 100 + hi[1]) - (lo[0] * 100 + lo[1]))
 
 
 @dataclass(frozen=True)
@@ -162,7 +172,7 @@ class Op:
         def add(fn: Callable) -> Callable:
             self._entries.append(_Entry(name, fn, device, frozenset(requires), priority, when, prepare, accepts,
                                         len(self._entries)))
-            self._entries.sort(key=lambda e: (-e.priority, e.seq))
+            self._entries.sort(key=lambda e: (-e.priority, e.device.span, e.seq))
             return fn
 
         return add

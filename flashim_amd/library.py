@@ -76,17 +76,19 @@ def _(value, exponent, padded):
 
 
 @torch.library.custom_op(f"{NS}::gelu_quantize_mxfp8", mutates_args=())
-def gelu_quantize_mxfp8(value: Tensor, exponent: Tensor, padded: int, input_bias: Optional[Tensor]) -> Tensor:
+def gelu_quantize_mxfp8(value: Tensor, exponent: Tensor, padded: int, input_bias: Optional[Tensor],
+                        tanh: bool = False) -> Tensor:
     out = torch.empty((*value.shape[:-1], padded), device=value.device, dtype=torch.uint8)
     x = as_4d(value)
-    _lib.call("fim_gelu_quantize_mxfp8", x.data_ptr(), _dtype_code(value), *x.shape, *x.stride(), _ptr(input_bias),
+    _lib.call("fim_gelu_quantize_mxfp8", x.data_ptr(), _dtype_code(value), *x.shape, *x.stride(), int(tanh),
+              _ptr(input_bias),
               exponent.data_ptr(), out.data_ptr(), padded, _stream(value),
               what=f"gelu_quantize_mxfp8 {tuple(value.shape)}")
     return out
 
 
 @gelu_quantize_mxfp8.register_fake
-def _(value, exponent, padded, input_bias):
+def _(value, exponent, padded, input_bias, tanh=False):
     return value.new_empty((*value.shape[:-1], padded), dtype=torch.uint8)
 
 
@@ -105,16 +107,17 @@ def _(value, scale, channel_scale):
 
 
 @torch.library.custom_op(f"{NS}::gelu_quantize_int8", mutates_args=())
-def gelu_quantize_int8(value: Tensor, scale: Tensor) -> Tensor:
+def gelu_quantize_int8(value: Tensor, scale: Tensor, tanh: bool = False) -> Tensor:
     out = torch.empty(value.shape, device=value.device, dtype=torch.int8)
     x = as_4d(value)
-    _lib.call("fim_gelu_quantize_int8", x.data_ptr(), _dtype_code(value), *x.shape, *x.stride(), scale.data_ptr(),
+    _lib.call("fim_gelu_quantize_int8", x.data_ptr(), _dtype_code(value), *x.shape, *x.stride(), int(tanh),
+              scale.data_ptr(),
               out.data_ptr(), _stream(value), what=f"gelu_quantize_int8 {tuple(value.shape)}")
     return out
 
 
 @gelu_quantize_int8.register_fake
-def _(value, scale):
+def _(value, scale, tanh=False):
     return value.new_empty(value.shape, dtype=torch.int8)
 
 

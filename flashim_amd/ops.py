@@ -20,6 +20,7 @@ from flashim_amd.platforms import Feature
 # declarations (FlashIM names)
 quantize_mxfp8 = Op("quantize_mxfp8")
 quantize_int8 = Op("quantize_int8")
+quantize_int8_rows = Op("quantize_int8_rows")
 gelu_quantize = Op("gelu_quantize")
 gelu_quantize_int8 = Op("gelu_quantize_int8")
 int8_conv2d = Op("int8_conv2d")
@@ -50,6 +51,7 @@ IMPLS = (
     # (op name, impl fn, required features, when)
     ("quantize_mxfp8", _quantize.quantize_mxfp8, (Feature.HIP, Feature.FP8_E4M3), _quantize.eligible_quantize_mxfp8),
     ("quantize_int8", _quantize.quantize_int8, (Feature.HIP,), _quantize.eligible_quantize_int8),
+    ("quantize_int8_rows", _quantize.quantize_int8_rows, (Feature.HIP,), _quantize.eligible_quantize_int8_rows),
     ("gelu_quantize", _quantize.gelu_quantize, (Feature.HIP, Feature.FP8_E4M3), _quantize.eligible_gelu_quantize),
     ("gelu_quantize_int8", _quantize.gelu_quantize_int8, (Feature.HIP,), _quantize.eligible_gelu_quantize_int8),
     ("int8_conv2d", _conv.int8_conv2d, _I8, _conv.eligible_int8_conv2d),

@@ -124,6 +124,7 @@ def impls(upstream_tensor_module) -> dict[str, tuple[Callable, Callable]]:
     return {
         "quantize_mxfp8": (quantize_mxfp8, _quantize.eligible_quantize_mxfp8),
         "quantize_int8": (quantize_int8, _quantize.eligible_quantize_int8),
+        "quantize_int8_rows": (_quantize.quantize_int8_rows, _quantize.eligible_quantize_int8_rows),
         "gelu_quantize": (gelu_quantize, _quantize.eligible_gelu_quantize),
         "gelu_quantize_int8": (gelu_quantize_int8, _quantize.eligible_gelu_quantize_int8),
         "int8_conv2d": (_conv.int8_conv2d, _conv.eligible_int8_conv2d),

@@ -141,9 +141,11 @@ def quantize_static(value: Tensor, scale_exponent: Tensor) -> QuantizedTensor:
     return QuantizedTensor(codes.view(torch.float8_e4m3fn), scale_exponent, tuple(value.shape))
 
 
-def gelu_quantize_static(value: Tensor, scale_exponent: Tensor, input_bias: Tensor | None = None) -> QuantizedTensor:
-    """``quantize_static(GELU(value [+ input_bias]))``, GELU (erf form) rounded to ``value``'s dtype
-    (``flashim/ops/quantize.py:63-74``)."""
+def gelu_quantize_static(value: Tensor, scale_exponent: Tensor, input_bias: Tensor | None = None,
+                         approximate: str = "none") -> QuantizedTensor:
+    """``quantize_static(GELU(value [+ input_bias]))``, GELU (``approximate`` "none": erf form, "tanh": tanh form)
+    rounded to ``value``'s dtype (``flashim/ops/quantize.py:63-74``)."""
+    tanh = _gelu_form(approximate)
     if value.ndim < 2:
         raise ValueError(f"Expected a channelized tensor, got {tuple(value.shape)}")
     _require_gpu(value, "gelu_quantize")
@@ -154,7 +156,7 @@ def gelu_quantize_static(value: Tensor, scale_exponent: Tensor, input_bias: Tens
         raise ValueError(f"Expected scale shape {(padded // BLOCK,)}, got {tuple(scale_exponent.shape)}")
     if input_bias is not None:
         input_bias = input_bias.to(device=value.device, dtype=torch.float32).contiguous()
-    codes = library.gelu_quantize_mxfp8(value, scale_exponent, padded, input_bias)
+    codes = library.gelu_quantize_mxfp8(value, scale_exponent, padded, input_bias, tanh)
     return QuantizedTensor(codes.view(torch.float8_e4m3fn), scale_exponent, tuple(value.shape))
 
 
@@ -174,12 +176,20 @@ def quantize_int8_static(value: Tensor, scale: Tensor) -> Int8Tensor:
     return Int8Tensor(quantize_int8_values(value, scale), scale)
 
 
-def gelu_quantize_int8_static(value: Tensor, scale: Tensor) -> Int8Tensor:
-    """``quantize_int8_static(GELU(value))``, GELU rounded to ``value``'s dtype (``flashim/ops/quantize.py:128-131``)."""
+def _gelu_form(approximate: str) -> bool:
+    if approximate not in ("none", "tanh"):
+        raise ValueError(f"approximate must be 'none' or 'tanh', got {approximate!r}")
+    return approximate == "tanh"
+
+
+def gelu_quantize_int8_static(value: Tensor, scale: Tensor, approximate: str = "none") -> Int8Tensor:
+    """``quantize_int8_static(GELU(value))``, GELU (erf or tanh form) rounded to ``value``'s dtype
+    (``flashim/ops/quantize.py:128-131``)."""
+    tanh = _gelu_form(approximate)
     _require_gpu(value, "gelu_quantize_int8")
     _dtype_code(value, "gelu_quantize_int8")
     scale = scale.to(device=value.device, dtype=torch.float32).reshape(())
-    return Int8Tensor(library.gelu_quantize_int8(value, scale.reshape(1)), scale)
+    return Int8Tensor(library.gelu_quantize_int8(value, scale.reshape(1), tanh), scale)
 
 
 def _dynamic_input(value: Tensor, what: str) -> Tensor:
@@ -213,6 +223,14 @@ def weight_scales_and_values(weight: Tensor) -> tuple[Tensor, Tensor]:
     _require_gpu(weight, "weight_scales")
     _dtype_code(weight, "weight_scales")
     return library.quantize_int8_rows(weight.contiguous(), False)
+
+
+def quantize_int8_rows(matrix: Tensor) -> tuple[Tensor, Tensor]:
+    """Per-row dynamic INT8 of a row-major ``[rows, K]`` matrix (unit column stride, any row stride): ``(q, scale)``
+    with ``scale = safe_scale(amax * float32(1 / 127))`` (``flashim/ops/quantize.py:148-154``)."""
+    _require_gpu(matrix, "quantize_int8_rows")
+    _dtype_code(matrix, "quantize_int8_rows")
+    return library.quantize_int8_rows(matrix, True)
 
 
 def calibrate_block32_exponent(value: Tensor) -> Tensor:

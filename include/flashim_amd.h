@@ -45,17 +45,19 @@ int fim_quantize_mxfp8(const void* x, int dtype, int64_t B, int64_t H, int64_t W
                        int64_t sw, int64_t sc, const int8_t* exponent, uint8_t* out, int64_t Cpad,
                        hipStream_t stream);
 
-/* GELU (erf form) then static block-32 MXFP8, fim_quantize_mxfp8's geometry and output: v = x (+ input_bias[c] in
- * FP32, input_bias may be NULL), g = gelu(v) in FP32 rounded to x's dtype, out = e4m3(clamp(g / 2^exponent[c/32],
- * +-448)). Replaces ops.gelu_quantize with approximate="none" (flashim/ops/quantize.py:63-74). */
+/* GELU then static block-32 MXFP8, fim_quantize_mxfp8's geometry and output: v = x (+ input_bias[c] in FP32,
+ * input_bias may be NULL), g = gelu(v) in FP32 rounded to x's dtype, out = e4m3(clamp(g / 2^exponent[c/32], +-448)).
+ * approximate: 0 the erf form, 1 the tanh form (F.gelu's approximate="none" / "tanh"; else 98).
+ * Replaces ops.gelu_quantize (flashim/ops/quantize.py:63-74). */
 int fim_gelu_quantize_mxfp8(const void* x, int dtype, int64_t B, int64_t H, int64_t W, int64_t C, int64_t sb,
-                            int64_t sh, int64_t sw, int64_t sc, const float* input_bias, const int8_t* exponent,
-                            uint8_t* out, int64_t Cpad, hipStream_t stream);
+                            int64_t sh, int64_t sw, int64_t sc, int approximate, const float* input_bias,
+                            const int8_t* exponent, uint8_t* out, int64_t Cpad, hipStream_t stream);
 
-/* GELU (erf form) in x's dtype then static per-tensor INT8 with *scale, fim_quantize_int8's geometry and output.
- * Replaces ops.gelu_quantize_int8 with approximate="none" (flashim/ops/quantize.py:128-131). */
+/* GELU (approximate as above) in x's dtype then static per-tensor INT8 with *scale, fim_quantize_int8's geometry and
+ * output. Replaces ops.gelu_quantize_int8 (flashim/ops/quantize.py:128-131). */
 int fim_gelu_quantize_int8(const void* x, int dtype, int64_t B, int64_t H, int64_t W, int64_t C, int64_t sb,
-                           int64_t sh, int64_t sw, int64_t sc, const float* scale, int8_t* out, hipStream_t stream);
+                           int64_t sh, int64_t sw, int64_t sc, int approximate, const float* scale, int8_t* out,
+                           hipStream_t stream);
 
 /* Dynamic per-(row, 32) MXFP8 of a [rows, K] matrix (K % 32 == 0, row stride in elements, 16-byte aligned rows):
  * E4M3 out [rows, K] (packed), exponent [rows, K/32] int8 (may be NULL), and the E8M0 scales in cuBLAS' 128x4
@@ -211,29 +213,6 @@ int fim_depthwise5x5_relu_pointwise_mxfp8(const uint16_t* x, int64_t B, int64_t 
  * it stands for is launch_depthwise5x5_relu_pointwise, flashim/backends/cuda/conv.py:194-209). */
 int fim_pointwise_bf16(const uint16_t* x, int64_t M, int64_t K, const uint16_t* weight, int64_t N, const float* bias,
                        uint16_t* out, hipStream_t stream);
-
-/* ---- test hooks ------------------------------------------------------------------------------------------------ */
-
-/* E4M3 encodings of n floats with the hardware conversion the kernels use (out[i]) and with the software encoder
- * (out[n + i]); x must be pre-clamped to +-448. Lets the tests check the two agree on the device. */
-int fim_test_e4m3(const float* x, int64_t n, uint8_t* out, hipStream_t stream);
-
-/* BF16 roundings of n floats with the hardware conversion the kernels use (out[i]) and with the software rule
- * (out[n + i]). */
-int fim_test_bf16(const float* x, int64_t n, uint16_t* out, hipStream_t stream);
-
-/* GELU (erf form) of n BF16 values as the kernels' epilogues evaluate it, BF16 out. */
-int fim_test_gelu(const uint16_t* x, int64_t n, uint16_t* out, hipStream_t stream);
-
-/* MX exponents of n FP32 amax values with the device rule (quant/formats/mx.py:22-26). */
-int fim_test_mx_exponent(const float* amax, int64_t n, int8_t* out, hipStream_t stream);
-
-/* MFMA throughput microbenchmark (no counterpart in the reference; the measured peak the roofline fractions are also
- * quoted against): `blocks` workgroups of 256 threads, each wavefront `iters` rounds of 8 independent 16 x 16 MFMAs on
- * register operands. kind 0: scaled MXFP8 16x16x128 (65536 FLOP each), 1: INT8 16x16x64 (32768 OP each), 2: INT8
- * 32x32x32 (65536 OP each). out: FP32
- * [blocks * 256], one sum per thread. */
-int fim_test_mfma_peak(int kind, int64_t blocks, int iters, float* out, hipStream_t stream);
 
 #ifdef __cplusplus
 }

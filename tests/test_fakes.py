@@ -94,6 +94,9 @@ def test_quantize_fakes_match_oracle_shapes():
     assert got_codes == _sig_mx(cv) and got_swz[0] == (ref.swizzle_scales(ce).numel(),)
     q, sc = ref.quantize_int8_rows(m)
     assert _fake_run(quant.weight_scales_and_values, m) == (_sig(q), ((300,), torch.float32))
+    m3 = torch.randn(2, 150, 64)
+    q3, s3 = ref.quantize_int8_rows(m3)
+    assert _fake_run(hq.quantize_int8_rows, m3) == (_sig(q3), _sig(s3))
     assert _fake_run(quant.calibrate_block32_exponent, v) == _sig(ref.calibrate_block32_exponent(v))
 
 

@@ -15,7 +15,7 @@ DEV = "cuda"
 def _device_e4m3(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     x = x.to(DEV).float().contiguous()
     out = torch.empty(2 * x.numel(), device=DEV, dtype=torch.uint8)
-    _lib.call("fim_test_e4m3", x.data_ptr(), x.numel(), out.data_ptr(), _lib.stream_of(x))
+    _lib.probe_call("fim_test_e4m3", x.data_ptr(), x.numel(), out.data_ptr(), _lib.stream_of(x))
     out = out.cpu()
     return out[: x.numel()], out[x.numel():]
 
@@ -45,7 +45,7 @@ def test_mx_exponent_matches_oracle():
     amax = amax[torch.isfinite(amax)].contiguous()
     out = torch.empty(amax.numel(), device=DEV, dtype=torch.int8)
     a = amax.to(DEV)
-    _lib.call("fim_test_mx_exponent", a.data_ptr(), a.numel(), out.data_ptr(), _lib.stream_of(a))
+    _lib.probe_call("fim_test_mx_exponent", a.data_ptr(), a.numel(), out.data_ptr(), _lib.stream_of(a))
     assert torch.equal(out.cpu(), ref.scale_exponent_from_amax(amax))
 
 
@@ -63,7 +63,7 @@ def test_bf16_hardware_rounding_matches_torch():
         x = x[torch.isfinite(x)].contiguous()
         xd = x.to(DEV)
         out = torch.empty(2 * x.numel(), device=DEV, dtype=torch.int16)
-        _lib.call("fim_test_bf16", xd.data_ptr(), x.numel(), out.data_ptr(), _lib.stream_of(xd))
+        _lib.probe_call("fim_test_bf16", xd.data_ptr(), x.numel(), out.data_ptr(), _lib.stream_of(xd))
         out = out.cpu()
         want = x.to(torch.bfloat16).view(torch.int16)
         assert torch.equal(out[x.numel():], want)
@@ -76,7 +76,7 @@ def test_gelu_within_one_bf16_rounding_of_torch_on_every_bf16_input():
     x = torch.arange(0, 65536, dtype=torch.int32).to(torch.int16)
     xd = x.to(DEV)
     out = torch.empty(65536, device=DEV, dtype=torch.int16)
-    _lib.call("fim_test_gelu", xd.data_ptr(), 65536, out.data_ptr(), _lib.stream_of(xd))
+    _lib.probe_call("fim_test_gelu", xd.data_ptr(), 65536, out.data_ptr(), _lib.stream_of(xd))
     xs = x.view(torch.bfloat16)
     want = torch.nn.functional.gelu(xs).float()
     got = out.cpu().view(torch.bfloat16).float()
@@ -91,6 +91,6 @@ def test_gelu_within_one_bf16_rounding_of_torch_on_every_bf16_input():
 def test_mfma_peak_hook_runs(kind):
     """The MFMA microbenchmark the bench quotes its measured peaks from: it runs and every thread's sum is finite."""
     out = torch.empty(4 * 256, device="cuda", dtype=torch.float32)
-    _lib.call("fim_test_mfma_peak", kind, 4, 10, out.data_ptr(), _lib.stream_of(out))
+    _lib.probe_call("fim_test_mfma_peak", kind, 4, 10, out.data_ptr(), _lib.stream_of(out))
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()

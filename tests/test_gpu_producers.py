@@ -6,7 +6,8 @@ flashim/ops/quantize.py:63-74, 128-131), ``ops.int8_linear_quantize`` into a str
 Bars: the packers and ``int8_linear_quantize`` are byte-exact. The GELU producers evaluate erf with this library's own
 fit, which agrees with torch's libm GELU within one BF16 rounding (about 1% of BF16 inputs land one step apart, and
 torch's FP32 ``1 + erf`` cancels below |GELU| ~ 4e-3): codes are compared after dequantizing, each within one code step
-of the oracle's value or an absolute 2^-12 (in the unscaled domain), and at most 0.5% of the codes may differ."""
+of the oracle's value or an absolute 2^-12 (in the unscaled domain), and at most 0.5% of the codes may differ. The tanh
+form is x / (1 + e^(-2y)), which avoids torch's 1 + tanh cancellation in the negative tail; same bars."""
 
 import pytest
 import torch
@@ -38,20 +39,21 @@ def _assert_mx_codes_close(got_codes, want_codes, exponent):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
 @pytest.mark.parametrize("shape", [(2, 17, 19, 64), (300, 96), (4, 9, 70)])
 @pytest.mark.parametrize("with_bias", [False, True])
-def test_gelu_quantize(shape, dtype, with_bias):
+@pytest.mark.parametrize("approximate", ["none", "tanh"])
+def test_gelu_quantize(shape, dtype, with_bias, approximate):
     torch.manual_seed(0)
     x = (torch.randn(shape) * 3).to(dtype)
     bias = torch.randn(shape[-1]) * 0.5 if with_bias else None
-    activated = F.gelu(x.float() + (bias if with_bias else 0)).to(dtype)
+    activated = F.gelu(x.float() + (bias if with_bias else 0), approximate=approximate).to(dtype)
     exponent = ref.calibrate_block32_exponent(activated.float())
-    got = ops.gelu_quantize.get("hip")(x.to(DEV), exponent.to(DEV),
+    got = ops.gelu_quantize.get("hip")(x.to(DEV), exponent.to(DEV), approximate,
                                        input_bias=None if bias is None else bias.to(DEV))
-    want = ref.gelu_quantize(x, exponent, input_bias=bias)
+    want = ref.gelu_quantize(x, exponent, approximate, input_bias=bias)
     assert got.values.shape == want.shape and got.logical_shape == tuple(shape)
     _assert_mx_codes_close(got.values.cpu(), want, exponent)
 
 
-def test_gelu_quantize_channels_first_view_and_tanh_refused():
+def test_gelu_quantize_channels_first_view_and_forms():
     torch.manual_seed(1)
     x = torch.randn(2, 64, 9, 11, dtype=torch.bfloat16) * 2
     view = x.to(DEV).permute(0, 2, 3, 1)
@@ -60,16 +62,24 @@ def test_gelu_quantize_channels_first_view_and_tanh_refused():
     packed = ops.gelu_quantize.get("hip")(view.contiguous(), exponent.to(DEV))
     assert torch.equal(got.values.view(torch.uint8), packed.values.view(torch.uint8))
     _assert_mx_codes_close(got.values.cpu(), ref.gelu_quantize(x.permute(0, 2, 3, 1), exponent), exponent)
-    assert not ops.gelu_quantize.supports(view, exponent.to(DEV), "tanh")
+    tanh = ops.gelu_quantize.get("hip")(view, exponent.to(DEV), "tanh")
+    _assert_mx_codes_close(tanh.values.cpu(), ref.gelu_quantize(x.permute(0, 2, 3, 1), exponent, "tanh"), exponent)
+    assert not ops.gelu_quantize.supports(view, exponent.to(DEV), "sigmoid")
+    # the forms part in the negative tail: GELU(-2.5) = -0.015084 (tanh) / -0.015524 (erf), INT8 codes -15 / -16 at 1e-3
+    tail = torch.full((1, 64), -2.5, device=DEV)
+    s = torch.tensor(1e-3, device=DEV)
+    assert ops.gelu_quantize_int8.get("hip")(tail, s, "tanh").values[0, 0].item() == -15
+    assert ops.gelu_quantize_int8.get("hip")(tail, s).values[0, 0].item() == -16
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_gelu_quantize_int8(dtype):
+@pytest.mark.parametrize("approximate", ["none", "tanh"])
+def test_gelu_quantize_int8(dtype, approximate):
     torch.manual_seed(2)
     x = (torch.randn(3, 33, 40, 48) * 2).to(dtype)
     scale = torch.tensor(0.021)
-    got = ops.gelu_quantize_int8.get("hip")(x.to(DEV), scale.to(DEV)).values.cpu()
-    want = ref.gelu_quantize_int8(x, scale)
+    got = ops.gelu_quantize_int8.get("hip")(x.to(DEV), scale.to(DEV), approximate).values.cpu()
+    want = ref.gelu_quantize_int8(x, scale, approximate)
     assert (got.int() - want.int()).abs().max() <= 1
     assert (got != want).float().mean() <= 5e-3
 

@@ -46,6 +46,41 @@ def test_quantize_int8_known_answer_and_channel_scale():
     assert torch.equal(got.values.cpu(), ref.quantize_int8(y, s, cs))
 
 
+def test_quantize_int8_channel_scale_multiplies():
+    """ops/quantize.py:91-97: value * channel_scale, then / scale (dividing by the channel scale gives [2, 12])."""
+    x = torch.tensor([[3.0, 3.0], [-3.0, 100.0]], device=DEV)
+    cs = torch.tensor([2.0, 0.25], device=DEV)
+    got = ops.quantize_int8.get("hip")(x, torch.tensor(1.0, device=DEV), channel_scale=cs)
+    assert got.values.cpu().tolist() == [[6, 1], [-6, 25]]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("rows,k", [(5376, 1024), (777, 4096), (300, 1000), (5, 64), (3, 7)])
+def test_quantize_int8_rows_bytes(rows, k, dtype):
+    """Per-row dynamic INT8 (ops/quantize.py:148-154): codes and scales bit-identical to the oracle, with an outlier
+    row and an all-zero row (FlashIM's contract, tests/ops/test_ops_cuda.py:967-979)."""
+    torch.manual_seed(0)
+    x = (torch.randn(rows, k) * 3).to(dtype)
+    x[rows // 2] *= 300
+    x[-1] = 0
+    got_q, got_s = ops.quantize_int8_rows.get("hip")(x.to(DEV))
+    want_q, want_s = ref.quantize_int8_rows(x)
+    assert got_s.shape == (rows, 1) and got_s.dtype == torch.float32
+    assert torch.equal(got_s.cpu(), want_s) and torch.equal(got_q.cpu(), want_q)
+
+
+def test_quantize_int8_rows_reciprocal_scale_known_answer():
+    """amax = 5.798794: amax * float32(1/127) and amax / 127 differ by one ulp, and 0.068489686 rounds to 2 only under
+    the reciprocal product, which the reference specifies."""
+    x = torch.tensor([[5.798794, 0.068489686, -0.068489686, 0.0]], device=DEV)
+    q, s = ops.quantize_int8_rows.get("hip")(x)
+    assert q.cpu().tolist() == [[127, 2, -2, 0]]
+    want_q, want_s = ref.quantize_int8_rows(x.cpu())
+    assert torch.equal(s.cpu(), want_s)
+    q3, s3 = ops.quantize_int8_rows.get("hip")(torch.randn(2, 3, 64, device=DEV, dtype=torch.bfloat16))
+    assert q3.shape == (2, 3, 64) and s3.shape == (2, 3, 1)
+
+
 @pytest.mark.parametrize("channels", [16, 48, 96, 257])
 @pytest.mark.parametrize("fmt", ["int8", "mxfp8"])
 def test_quantize_channels_first_view(channels, fmt):

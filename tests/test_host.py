@@ -33,6 +33,20 @@ def test_library_exports_every_declared_symbol():
     assert lib.fim_version() >= 100
 
 
+def test_probes_live_in_their_own_library():
+    """The test / measurement hooks are built into libflashim_amd_probe.so, not the product library or its header."""
+    header = (ROOT / "include" / "flashim_amd.h").read_text()
+    assert "fim_test_" not in header
+    probe_header = (ROOT / "flashim_amd" / "csrc" / "probe.h").read_text()
+    declared = set(re.findall(r"^int (fim_\w+)\(", probe_header, re.M))
+    assert declared == set(_lib.PROBE_SIGNATURES)
+    probe, lib = _lib.load_probe(), _lib.load()
+    for name in declared:
+        assert hasattr(probe, name), name
+        with pytest.raises(AttributeError):
+            getattr(lib, name)
+
+
 def test_header_compiles_as_c():
     import subprocess
 
@@ -163,6 +177,23 @@ def test_dispatch_order_when_optin_and_pins():
         op.get("missing")
     with pytest.raises(ValueError):
         op.register("low", device=dispatch.DeviceSpec("cpu"))
+
+
+@pytest.mark.parametrize("wildcard_first", [True, False])
+def test_dispatch_ties_prefer_the_narrower_device_spec(wildcard_first):
+    """Equal priority: the platform-specific impl beats a '*' impl whatever the registration order, as FlashIM's
+    registry sorts by (priority, capability span, order) (flashim/ops/_registry.py:62-68, 214)."""
+    name = f"toy_span_{wildcard_first}"
+    dispatch.OPS.pop(name, None)
+    op = dispatch.Op(name)
+    specs = [("any", dispatch.DeviceSpec("*")), ("cpu", dispatch.DeviceSpec("cpu"))]
+    for impl, spec in (specs if wildcard_first else specs[::-1]):
+        op.register(impl, device=spec, priority=1)(lambda x, impl=impl: impl)
+    op.register("narrow", device=dispatch.DeviceSpec("cpu"), priority=0)(lambda x: "narrow")
+    assert op(torch.tensor(1.0)) == "cpu"
+    assert [e.name for e in op.impls] == ["cpu", "any", "narrow"]  # priority still decides first
+    assert dispatch.DeviceSpec("*").span == float("inf")
+    assert dispatch.DeviceSpec("cuda", (8, 0), (9, 0)).span == 100.0 < dispatch.DeviceSpec("cuda").span
 
 
 def test_dispatch_overrides_and_counts():

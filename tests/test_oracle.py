@@ -121,6 +121,45 @@ def test_int8_quantize_is_one_ieee_division():
     assert q.item() == int(np.rint(exact))
 
 
+def test_int8_channel_scale_multiplies_before_the_division():
+    # ops/quantize.py:91-97: value * channel_scale (SmoothQuant's 1 / s), then round(. / scale). Dividing by the channel
+    # scale instead would give [2, 12]; applying it after the rounding would give [6, 0] (round(3) * 0.25 -> 1 -> ...).
+    x = torch.tensor([[3.0, 3.0], [-3.0, 100.0]])
+    q = ref.quantize_int8(x, torch.tensor(1.0), torch.tensor([2.0, 0.25]))
+    assert q.tolist() == [[6, 1], [-6, 25]]
+    # scale and channel scale compose as (x * cs) / s: 10 * 0.5 / 0.25 = 20 (x / (cs * s) would give 80)
+    assert ref.quantize_int8(torch.tensor([10.0]), torch.tensor(0.25), torch.tensor([0.5])).tolist() == [20]
+    # saturation applies after the channel scale
+    assert ref.quantize_int8(torch.tensor([100.0]), torch.tensor(1.0), torch.tensor([3.0])).tolist() == [127]
+
+
+def test_quantize_int8_rows_reciprocal_scale():
+    # ops/quantize.py:148-154: scale = amax * float32(1 / 127), not amax / 127. For amax = 5.798794 the two differ by
+    # one FP32 ulp (0.04565979 against 0.045659795), and x = 0.068489686 then rounds to 2 under the reciprocal-product
+    # scale but to 1 under the divided one.
+    amax, x = np.float32("5.798794"), np.float32("0.068489686")
+    recip = np.float32(amax * np.float32(np.float32(1) / np.float32(127)))
+    divided = np.float32(amax / np.float32(127))
+    assert recip != divided and np.rint(x / recip) == 2 and np.rint(x / divided) == 1
+    rows = torch.tensor([[float(amax), float(x), -float(x), 0.0], [0.0, 0.0, 0.0, 0.0], [-1000.0, 2.0, 0.5, 1e-9]])
+    q, s = ref.quantize_int8_rows(rows)
+    assert s.shape == (3, 1) and s.dtype == torch.float32
+    assert s[0, 0].item() == float(recip)
+    assert q[0].tolist() == [127, 2, -2, 0]
+    # all-zero row: safe_scale -> FP32 eps, codes 0 (tests/ops/test_ops_cuda.py:967-979 zeroes the last row)
+    assert s[1, 0].item() == torch.finfo(torch.float32).eps and q[1].abs().sum() == 0
+    # the row's amax element saturates to exactly -127/127 and every code is within half a step of the value
+    assert q[2, 0].item() == -127
+    assert ((q[2].double() * s[2, 0].double() - rows[2].double()).abs() <= s[2, 0].double() / 2).all()
+    # per row: each row is scaled by its own amax (a transposed reduction would mix rows 0 and 2)
+    torch.manual_seed(0)
+    m = torch.randn(64, 96) * 3
+    m[5] *= 300
+    q, s = ref.quantize_int8_rows(m)
+    assert torch.equal(q.abs().amax(1), torch.full((64,), 127, dtype=torch.int8))
+    assert ((q.double() * s.double() - m.double()).abs() <= s.double() / 2 + 1e-12).all()
+
+
 def test_weight_scales_per_channel():
     # tests/quant/test_int8.py:14-21
     torch.manual_seed(0)
@@ -423,6 +462,34 @@ def test_gelu_quantize_producers_against_float64(dtype):
     g = _gelu64(x.double().numpy()).astype(np.float32)
     g = _bf16_np(g) if dtype == torch.bfloat16 else g
     assert np.abs(gi - np.clip(np.rint(g / np.float32(0.05)), -127, 127)).max() <= 1
+
+
+def _gelu_tanh64(x: np.ndarray) -> np.ndarray:
+    """0.5 x (1 + tanh(sqrt(2 / pi) (x + 0.044715 x^3))) in float64."""
+    return 0.5 * x * (1.0 + np.tanh(math.sqrt(2.0 / math.pi) * (x + 0.044715 * x**3)))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_gelu_quantize_tanh_form_against_float64(dtype):
+    """approximate="tanh" reaches F.gelu's tanh form (ops/quantize.py:63-74, 128-131), not the erf form: at x = 1 the
+    two differ by 1.5e-4 (0.841192 against 0.841345)."""
+    assert abs(_gelu_tanh64(np.array([1.0]))[0] - 0.8411919906082768) < 1e-15
+    x = torch.linspace(-6, 6, 4800).reshape(75, 64).to(dtype)
+    s = torch.tensor(0.05)
+    g = _gelu_tanh64(x.double().numpy()).astype(np.float32)
+    g = _bf16_np(g) if dtype == torch.bfloat16 else g
+    gi = ref.gelu_quantize_int8(x, s, approximate="tanh").numpy()
+    want = np.clip(np.rint(g / np.float32(0.05)), -127, 127)
+    assert np.abs(gi - want).max() <= 1 and (gi != want).mean() < 1e-2
+    e = torch.tensor([-6, -6], dtype=torch.int8)
+    got = ref.gelu_quantize(x, e, approximate="tanh").view(torch.float8_e4m3fn).double() * 2**-6
+    exact = torch.from_numpy(g).double()
+    assert ((got - exact).abs() <= exact.abs() * 2**-4 + 2**-6 * 2**-9).all()
+    # the forms part in the negative tail: GELU(-2.5) is -0.015084 (tanh) against -0.015524 (erf), codes -15 / -16
+    # at scale 1e-3
+    tail = torch.full((1, 64), -2.5)
+    assert ref.gelu_quantize_int8(tail, torch.tensor(1e-3), approximate="tanh")[0, 0].item() == -15
+    assert ref.gelu_quantize_int8(tail, torch.tensor(1e-3))[0, 0].item() == -16
 
 
 def test_int8_linear_quantize_is_the_requantized_linear():

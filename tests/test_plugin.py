@@ -40,7 +40,7 @@ class _StubOp:
         return add
 
 
-OP_NAMES = ("quantize_mxfp8", "quantize_int8", "gelu_quantize", "gelu_quantize_int8", "int8_conv2d", "mxfp8_conv2d",
+OP_NAMES = ("quantize_mxfp8", "quantize_int8", "quantize_int8_rows", "gelu_quantize", "gelu_quantize_int8", "int8_conv2d", "mxfp8_conv2d",
             "depthwise5x5_relu_mxfp8", "depthwise5x5_relu_int8", "depthwise5x5_relu_pointwise",
             "depthwise5x5_relu_pointwise_mxfp8",
             "depthwise5x5_relu_pointwise_int8", "im2col_gather", "int8_conv2d_maxpool", "int8_linear",
