@@ -97,30 +97,28 @@ __device__ __forceinline__ uint8_t e4m3(float a) {
 }
 
 // GELU, erf form: 0.5 x erfc(-x / sqrt 2) = max(x, 0) - |x| E with E = erfc(|x| / sqrt 2) / 2 (x >= 0: x - x E;
-// x < 0: x E). With z = |x| / sqrt 2 and t = 2 z / 4.1 - 1, log2 E is the degree-8 polynomial P(t) below (Chebyshev
-// fit of log2 erfc on [0, 4.1], minus 1), so E = 2^P(t): one v_exp_f32, 8 FMAs, no division, and the last step is one
-// FMA, fma(-|x|, E, max(x, -0)). The polynomial needs no clamp outside the fit: P is monotonically decreasing for
-// t > 1 and stays within 0.5 of log2 E up to |x| = 10 (E < 2^-77 there; P reaches -880 at |x| = 20 and -inf once its
-// leading term overflows), so the large-|x| limits come out right by themselves: x - 0 = x for large positive x, and
-// -0 (fma(-|x|, 0, -0)) once 2^P underflows for large negative x. Between x = -5.53 (where torch's FP32 1 + erf(x / sqrt 2)
-// becomes exactly 0, so torch returns -0) and about x = -12 the result is the true tiny GELU value (< 1e-7 in magnitude)
-// instead of -0. Against torch's BF16 GELU it differs by one BF16 step in about 1% of the finite BF16 inputs (torch's own
-// erf rounding moves values across BF16 rounding boundaries too); in torch's cancelling negative tail (x < -3) both are
-// within 2^-12 of each other. Signed zeros follow torch: GELU(+0) = +0, GELU(-0) = -0.
+// x < 0: x E). With z = |x| / sqrt 2 and t = 2 z / 4.1 - 1, log2 E is the degree-7 polynomial P(t) below (a near-minimax
+// fit of log2(erfc(z) / 2) on [0, 4.1], this repository's own, max error 4.7e-6 in log2 units, i.e. 3.3e-6 relative in
+// E), so E = 2^P(t): one v_exp_f32, 7 FMAs, no division, and the last step is one FMA, fma(-|x|, E, max(x, -0)). The
+// polynomial needs no clamp outside the fit: its leading coefficient is negative and P decreases monotonically for
+// t > 1 (P = -28.2 at the fit's end, below -900 at |x| = 40, -inf once its leading term overflows), so the large-|x|
+// limits come out right by themselves: x - 0 = x for large positive x, and -0 (fma(-|x|, 0, -0)) once 2^P underflows for
+// large negative x. Between x = -5.53 (where torch's FP32 1 + erf(x / sqrt 2) becomes exactly 0, so torch returns -0)
+// and about x = -12 the result is the true tiny GELU value (< 1e-7 in magnitude) instead of -0. Against torch's BF16
+// GELU it differs by one BF16 step in about 1% of the finite BF16 inputs (torch's own erf rounding moves values across
+// BF16 rounding boundaries too; the degree-8 fit this replaced differed on the same fraction); in torch's cancelling
+// negative tail (x < -3) both are within 2^-12 of each other. Signed zeros follow torch: GELU(+0) = +0, GELU(-0) = -0.
+// Evaluated in the rescaled variable u = s t, s = |c7|^(1/7) = 0.43911893, where the polynomial is monic up to sign
+// (coefficients c_k / s^k): its first Horner step is one subtraction with one literal, and u = |x| s sqrt(2) / 4.1 - s
+// is one FMA.
+constexpr float kGeluS = 0.43911893f, kGeluU = 0.15146535f;  // s, s sqrt(2) / 4.1
+constexpr float kGeluC[6] = {-2.2946658f, 2.3185021f, -2.3095699f, -29.120948f, -30.379971f,
+                             -9.0620125f};  // c6 / s^6 .. c0 (c0 includes the -1 of the factor 1/2)
 __device__ __forceinline__ float gelu_erf(float x) {
-  // Evaluated in the rescaled variable u = s t, s = |c8|^(1/8) = 0.3224875, so the polynomial is monic up to sign
-  // (coefficients c_k / s^k): its first Horner step is one subtraction with one literal (no constant kept in a
-  // register). u = |x| / sqrt 2 * 2 s / 4.1 - s as one FMA.
-  constexpr float kS = 0.3224875f;
-  const float u = fmaf(fabsf(x), 0.70710678118654752440f * 0.48780487804878f * kS, -kS);
-  float p = -9.393265f - u;
-  p = fmaf(p, u, 13.051149f);
-  p = fmaf(p, u, -10.621295f);
-  p = fmaf(p, u, 7.961414f);
-  p = fmaf(p, u, -5.8366094f);
-  p = fmaf(p, u, -53.993702f);
-  p = fmaf(p, u, -41.367184f);
-  p = fmaf(p, u, -9.062012672f);  // the fit's constant -8.062 minus 1: the factor 1/2
+  const float u = fmaf(fabsf(x), kGeluU, -kGeluS);
+  float p = 2.019375f - u;  // -u^7 + (c6 / s^6) u^6: the first Horner step
+#pragma unroll
+  for (int k = 0; k < 6; ++k) p = fmaf(p, u, kGeluC[k]);
   return fmaf(-fabsf(x), __builtin_amdgcn_exp2f(p), __builtin_elementwise_maximum(x, -0.0f));
 }
 
@@ -141,17 +139,15 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 // two at a time, and the VALU waits on the chain latency. Same arithmetic per value as gelu_erf.
 template <int N>
 __device__ __forceinline__ void gelu_erf_n(float (&x)[N]) {
-  constexpr float kS = 0.3224875f;
-  constexpr float kC[7] = {13.051149f, -10.621295f, 7.961414f, -5.8366094f, -53.993702f, -41.367184f, -9.062012672f};
   float u[N], p[N];
 #pragma unroll
-  for (int i = 0; i < N; ++i) u[i] = fmaf(fabsf(x[i]), 0.70710678118654752440f * 0.48780487804878f * kS, -kS);
+  for (int i = 0; i < N; ++i) u[i] = fmaf(fabsf(x[i]), kGeluU, -kGeluS);
 #pragma unroll
-  for (int i = 0; i < N; ++i) p[i] = -9.393265f - u[i];
+  for (int i = 0; i < N; ++i) p[i] = 2.019375f - u[i];
 #pragma unroll
-  for (int k = 0; k < 7; ++k)
+  for (int k = 0; k < 6; ++k)
 #pragma unroll
-    for (int i = 0; i < N; ++i) p[i] = fmaf(p[i], u[i], kC[k]);
+    for (int i = 0; i < N; ++i) p[i] = fmaf(p[i], u[i], kGeluC[k]);
 #pragma unroll
   for (int i = 0; i < N; ++i) x[i] = fmaf(-fabsf(x[i]), __builtin_amdgcn_exp2f(p[i]), __builtin_elementwise_maximum(x[i], -0.0f));
 }

@@ -26,6 +26,8 @@
 //   ops/gemm.py:94-95), optional residual relu(y + r) in FP32 then BF16 (ops/conv.py:198-203), then the store as
 //   BF16, or quantized for the next layer: INT8 with out_scale (quant/tensor.py:148-151) or E4M3 with out_exponent
 //   (quant/tensor.py:97-121).
+#include <type_traits>
+
 #include "common.h"
 
 namespace fim {
@@ -159,7 +161,8 @@ __device__ __forceinline__ EpiChannels<NB> epi_channels(int nl0, const float* ep
 // pixel, 16-byte slot s of row p at slot s ^ stage_swz(p) (the caller writes the tile out in whole lines).
 __device__ __forceinline__ int stage_swz(int p) { return (p >> 1) & 7; }
 
-template <int KIND, int OUT, int MB, int NB, bool GELU, bool RES = false, int STAGE_RB = 0>
+// GELU: 0 none (ReLU or the identity as one IEEE maximum), 1 GELU without ReLU (no maximum), 2 ReLU then GELU.
+template <int KIND, int OUT, int MB, int NB, int GELU, bool RES = false, int STAGE_RB = 0>
 __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
                                                    const v4f (&acc_f)[NB][MB], const int (&mrow)[MB], int n_tile0,
                                                    int nl0, const EpiChannels<NB>& ch, uint8_t* stage = nullptr,
@@ -226,7 +229,7 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
         else
           t = acc_f[i][j][e];
         t = __fadd_rn(t, cb[i][e]);  // the staged bias is -0 when there is none
-        v[e] = __builtin_elementwise_maximum(t, relu_lo);
+        v[e] = GELU == 1 ? t : __builtin_elementwise_maximum(t, relu_lo);
       }
       round_bf16x2(v[0], v[1]);
       round_bf16x2(v[2], v[3]);
@@ -291,41 +294,57 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
   }
 }
 
-// The fast epilogue's variants (GELU, dense residual) for lane rows mrow; the caller has checked conv_fast_ok.
+// The fast epilogue's variants (GELU with or without a ReLU before it, dense residual) for lane rows mrow, into global
+// memory (STAGE_RB = 0) or an LDS staging tile (see conv_epilogue_fast's STAGE_RB); the caller has checked
+// conv_fast_ok.
+template <int KIND, int OUT, int MB, int NB, int STAGE_RB = 0>
+__device__ __forceinline__ void conv_epilogue_any(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
+                                                  const v4f (&acc_f)[NB][MB], const int (&mrow)[MB], int n_tile0,
+                                                  int nl0, const EpiChannels<NB>& ch, uint8_t* stage = nullptr,
+                                                  const int* spix = nullptr) {
+#define FIM_EPI(G, R) \
+  conv_epilogue_fast<KIND, OUT, MB, NB, G, R, STAGE_RB>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch, stage, spix)
+  const int act = a.gelu ? (a.relu_pre ? 2 : 1) : 0;
+  if (a.residual != nullptr) {
+    if (act == 1) FIM_EPI(1, true);
+    else if (act == 2) FIM_EPI(2, true);
+    else FIM_EPI(0, true);
+  } else {
+    if (act == 1) FIM_EPI(1, false);
+    else if (act == 2) FIM_EPI(2, false);
+    else FIM_EPI(0, false);
+  }
+#undef FIM_EPI
+}
+
+// Calls f(integral_constant<int, GELU>, integral_constant<bool, RES>) with the fast epilogue's variant for this launch:
+// kernels whose epilogue is a loop of calls select the variant once, outside the loop, so the loop body holds one
+// variant and unrolls (with the selection inside, the body holds all six and the compiler stops unrolling, which turns
+// the accumulator indexing dynamic and puts the accumulators in scratch memory).
+template <typename F>
+__device__ __forceinline__ void with_epilogue_variant(const ConvArgs& a, F&& f) {
+  using G0 = std::integral_constant<int, 0>;
+  using G1 = std::integral_constant<int, 1>;
+  using G2 = std::integral_constant<int, 2>;
+  using RY = std::integral_constant<bool, true>;
+  using RN = std::integral_constant<bool, false>;
+  const int act = a.gelu ? (a.relu_pre ? 2 : 1) : 0;
+  if (a.residual != nullptr) {
+    if (act == 1) f(G1{}, RY{});
+    else if (act == 2) f(G2{}, RY{});
+    else f(G0{}, RY{});
+  } else {
+    if (act == 1) f(G1{}, RN{});
+    else if (act == 2) f(G2{}, RN{});
+    else f(G0{}, RN{});
+  }
+}
+
 template <int KIND, int OUT, int MB, int NB>
 __device__ __forceinline__ void conv_epilogue_rows(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
                                                    const v4f (&acc_f)[NB][MB], const int (&mrow)[MB], int n_tile0,
                                                    int nl0, const EpiChannels<NB>& ch) {
-  if (a.residual != nullptr) {
-    if (a.gelu)
-      conv_epilogue_fast<KIND, OUT, MB, NB, true, true>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch);
-    else
-      conv_epilogue_fast<KIND, OUT, MB, NB, false, true>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch);
-  } else if (a.gelu) {
-    conv_epilogue_fast<KIND, OUT, MB, NB, true>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch);
-  } else {
-    conv_epilogue_fast<KIND, OUT, MB, NB, false>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch);
-  }
-}
-
-// The same into an LDS staging tile (see conv_epilogue_fast's STAGE_RB).
-template <int KIND, int OUT, int MB, int NB, int STAGE_RB>
-__device__ __forceinline__ void conv_epilogue_rows_staged(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
-                                                          const v4f (&acc_f)[NB][MB], const int (&mrow)[MB],
-                                                          int n_tile0, int nl0, const EpiChannels<NB>& ch,
-                                                          uint8_t* stage, const int* spix) {
-  if (a.residual != nullptr) {
-    if (a.gelu)
-      conv_epilogue_fast<KIND, OUT, MB, NB, true, true, STAGE_RB>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch, stage, spix);
-    else
-      conv_epilogue_fast<KIND, OUT, MB, NB, false, true, STAGE_RB>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch, stage,
-                                                                   spix);
-  } else if (a.gelu) {
-    conv_epilogue_fast<KIND, OUT, MB, NB, true, false, STAGE_RB>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch, stage, spix);
-  } else {
-    conv_epilogue_fast<KIND, OUT, MB, NB, false, false, STAGE_RB>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch, stage,
-                                                                  spix);
-  }
+  conv_epilogue_any<KIND, OUT, MB, NB>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch);
 }
 
 template <int KIND, int OUT, int MB, int NB>
@@ -1423,42 +1442,46 @@ __global__ __launch_bounds__(512, 1) void conv_patch_kernel(const ConvArgs a) {
     uint8_t* const my_stage = stage + wq * (SPIX * RB);
     const int sl = lane % LPP;
     const bool cvalid = n0 + sl * (16 / ESZ) < a.Cout;
+    with_epilogue_variant(a, [&](auto gv, auto rv) __attribute__((always_inline)) {
+      constexpr int G = decltype(gv)::value;
+      constexpr bool R = decltype(rv)::value;
 #pragma unroll
-    for (int r = 0; r < SROUNDS; ++r) {
-      constexpr int RMB = MB / SROUNDS;  // pixel blocks per round
-      static_assert(RMB * SROUNDS == MB, "rounds split the blocks");
-      int mrow[RMB], spix[RMB];
-      v4i ai[NB][RMB];
-      v4f af[NB][RMB];
+      for (int r = 0; r < SROUNDS; ++r) {
+        constexpr int RMB = MB / SROUNDS;  // pixel blocks per round
+        static_assert(RMB * SROUNDS == MB, "rounds split the blocks");
+        int mrow[RMB], spix[RMB];
+        v4i ai[NB][RMB];
+        v4f af[NB][RMB];
 #pragma unroll
-      for (int j = 0; j < RMB; ++j) {
-        const int p = wq * (MB * 16) + (r * RMB + j) * 16 + (lane & 15);
-        const int oy = oy0 + p / TW, ox = ox0 + p % TW;
-        mrow[j] = (oy < a.Ho && ox < a.Wo) ? (img * a.Ho + oy) * a.Wo + ox : a.M;
-        spix[j] = j * 16 + (lane & 15);
+        for (int j = 0; j < RMB; ++j) {
+          const int p = wq * (MB * 16) + (r * RMB + j) * 16 + (lane & 15);
+          const int oy = oy0 + p / TW, ox = ox0 + p % TW;
+          mrow[j] = (oy < a.Ho && ox < a.Wo) ? (img * a.Ho + oy) * a.Wo + ox : a.M;
+          spix[j] = j * 16 + (lane & 15);
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-          ai[i][j] = acc_i[i][r * RMB + j];
-          af[i][j] = acc_f[i][r * RMB + j];
+          for (int i = 0; i < NB; ++i) {
+            ai[i][j] = acc_i[i][r * RMB + j];
+            af[i][j] = acc_f[i][r * RMB + j];
+          }
         }
-      }
-      conv_epilogue_rows_staged<KIND, OUT, RMB, NB, RB>(a, ai, af, mrow, n0, 0, ch, my_stage, spix);
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));  // this wavefront's staged rows (LDS ops run in order)
+        conv_epilogue_fast<KIND, OUT, RMB, NB, G, R, RB>(a, ai, af, mrow, n0, 0, ch, my_stage, spix);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));  // this wavefront's staged rows (LDS ops run in order)
 #pragma unroll
-      for (int c = 0; c < SCH; ++c) {
-        const int pl = c * PPC + lane / LPP;                              // pixel within the round
-        const int p = wq * (MB * 16) + r * SPIX + pl;                     // pixel within the tile
-        typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-        const u32x4 v = *reinterpret_cast<const u32x4*>(my_stage + pl * RB + ((sl ^ stage_swz(pl)) & (LPP - 1)) * 16);
-        const int oy = oy0 + p / TW, ox = ox0 + p % TW;
-        const bool ok = cvalid && oy < a.Ho && ox < a.Wo;
-        const uint32_t off =
-            ok ? ((uint32_t)((img * a.Ho + oy) * a.Wo + ox) * (uint32_t)a.out_ld + (uint32_t)n0) * ESZ + sl * 16
-               : OOB;
-        __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, (int)off, 0, 0);
+        for (int c = 0; c < SCH; ++c) {
+          const int pl = c * PPC + lane / LPP;                              // pixel within the round
+          const int p = wq * (MB * 16) + r * SPIX + pl;                     // pixel within the tile
+          typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+          const u32x4 v = *reinterpret_cast<const u32x4*>(my_stage + pl * RB + ((sl ^ stage_swz(pl)) & (LPP - 1)) * 16);
+          const int oy = oy0 + p / TW, ox = ox0 + p % TW;
+          const bool ok = cvalid && oy < a.Ho && ox < a.Wo;
+          const uint32_t off =
+              ok ? ((uint32_t)((img * a.Ho + oy) * a.Wo + ox) * (uint32_t)a.out_ld + (uint32_t)n0) * ESZ + sl * 16
+                 : OOB;
+          __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, (int)off, 0, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));  // the staged rows read before the next round overwrites them
       }
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));  // the staged rows read before the next round overwrites them
-    }
+    });
     if (next < total) wait_vm_at_most(SROUNDS * SCH);  // this wavefront's patch loads, issued before its stores
   };
 
@@ -1727,39 +1750,44 @@ __global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
     const int m0 = (t / a.n_tiles) * (8 * TMW) + wave * TMW;
     const int sl = lane % LPP;
     const bool cvalid = n0 + sl * (16 / ESZ) < a.Cout;
+    with_epilogue_variant(a, [&](auto gv, auto rv) __attribute__((always_inline)) {
+      constexpr int G = decltype(gv)::value;
+      constexpr bool R = decltype(rv)::value;
 #pragma unroll
-    for (int r = 0; r < MB; ++r) {
-      int mrow[1], spix[1];
-      const int m = m0 + r * 16 + (lane & 15);
-      mrow[0] = m < a.M ? m : a.M;
-      spix[0] = lane & 15;
+      for (int r = 0; r < MB; ++r) {
+        int mrow[1], spix[1];
+        const int m = m0 + r * 16 + (lane & 15);
+        mrow[0] = m < a.M ? m : a.M;
+        spix[0] = lane & 15;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {  // channel halves: 4 blocks' per-channel operands in registers at a time
-        int eo = 0;
-        asm volatile("" : "+v"(eo));
-        const EpiChannels<4> ch = epi_channels<4>(64 * h, ep_scale + eo, ep_bias + eo, ep_osc + eo);
-        v4i ai[4][1];
-        v4f af[4][1];
+        for (int h = 0; h < 2; ++h) {  // channel halves: 4 blocks' per-channel operands in registers at a time
+          int eo = 0;
+          asm volatile("" : "+v"(eo));
+          const EpiChannels<4> ch = epi_channels<4>(64 * h, ep_scale + eo, ep_bias + eo, ep_osc + eo);
+          v4i ai[4][1];
+          v4f af[4][1];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          ai[i][0] = acc_i[4 * h + i][r];
-          af[i][0] = acc_f[4 * h + i][r];
+          for (int i = 0; i < 4; ++i) {
+            ai[i][0] = acc_i[4 * h + i][r];
+            af[i][0] = acc_f[4 * h + i][r];
+          }
+          conv_epilogue_fast<KIND, OUT, 1, 4, G, R, RB>(a, ai, af, mrow, n0, 64 * h, ch, my_stage, spix);
         }
-        conv_epilogue_rows_staged<KIND, OUT, 1, 4, RB>(a, ai, af, mrow, n0, 64 * h, ch, my_stage, spix);
-      }
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
 #pragma unroll
-      for (int c = 0; c < SCH; ++c) {
-        const int pl = c * PPC + lane / LPP;
-        typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-        const u32x4 v = *reinterpret_cast<const u32x4*>(my_stage + pl * RB + ((sl ^ stage_swz(pl)) & (LPP - 1)) * 16);
-        const int mm = m0 + r * 16 + pl;
-        const uint32_t off = cvalid && mm < a.M ? ((uint32_t)mm * (uint32_t)a.out_ld + (uint32_t)n0) * ESZ + sl * 16
-                                                : OOB;
-        __builtin_amdgcn_raw_buffer_store_b128(v, orsrc, (int)off, 0, 0);
+        for (int c = 0; c < SCH; ++c) {
+          const int pl = c * PPC + lane / LPP;
+          typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+          const u32x4 v =
+              *reinterpret_cast<const u32x4*>(my_stage + pl * RB + ((sl ^ stage_swz(pl)) & (LPP - 1)) * 16);
+          const int mm = m0 + r * 16 + pl;
+          const uint32_t off =
+              cvalid && mm < a.M ? ((uint32_t)mm * (uint32_t)a.out_ld + (uint32_t)n0) * ESZ + sl * 16 : OOB;
+          __builtin_amdgcn_raw_buffer_store_b128(v, orsrc, (int)off, 0, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
       }
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
-    }
+    });
   };
 
   for (int t = first; t < total; t += stride) run_tile(t);
