@@ -426,6 +426,11 @@ PATCH_CASES = [
     ("3x3_pad0", (1, 33, 41), 128, 48, (3, 3, 1, 1, 0, 0, 1, 1)),
     ("3x3_n256_many_tiles", (3, 64, 120), 128, 256, (3, 3, 1, 1, 1, 1, 1, 1)),
     ("3x3_pad2", (1, 20, 30), 128, 64, (3, 3, 1, 1, 2, 2, 1, 1)),
+    # larger images: several tiles per workgroup and group (partial tiles at both image edges, a partial channel
+    # block, padding 0)
+    ("3x3_wg_tiles", (2, 150, 170), 128, 128, (3, 3, 1, 1, 1, 1, 1, 1)),
+    ("3x3_wg_tiles_n96", (3, 120, 130), 128, 96, (3, 3, 1, 1, 1, 1, 1, 1)),
+    ("3x3_wg_tiles_pad0", (3, 130, 140), 128, 128, (3, 3, 1, 1, 0, 0, 1, 1)),
 ]
 
 
