@@ -34,11 +34,14 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, p);
 }
 
-// a and b rounded to BF16 and widened back (torch's `.to(torch.bfloat16).float()` on each).
+// x rounded to BF16 and widened back (torch's `.to(torch.bfloat16).float()`): one v_cvt_pk_bf16_f32 with a zero low
+// half, whose 32-bit result is the rounded value itself (no unpacking).
+__device__ __forceinline__ float round_bf16_hw(float x) { return u2f(pack_bf16x2(0.0f, x)); }
+
+// a and b rounded to BF16 and widened back: two conversions (cheaper than one packed conversion and two unpacks).
 __device__ __forceinline__ void round_bf16x2(float& a, float& b) {
-  const uint32_t p = pack_bf16x2(a, b);
-  a = u2f(p << 16);
-  b = u2f(p & 0xffff0000u);
+  a = round_bf16_hw(a);
+  b = round_bf16_hw(b);
 }
 
 template <int DT>

@@ -469,7 +469,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc
                                                       : static_cast<const float*>(a.residual)[off];
               float t = __fadd_rn(y[v], r);
               if (relu_post) t = fmaxf(t, 0.0f);
-              y[v] = round_bf16(t);
+              y[v] = round_bf16_hw(t);
             } else if (relu_post) {
               y[v] = fmaxf(y[v], 0.0f);
             }
@@ -1858,8 +1858,15 @@ __global__ __launch_bounds__(512, 1) void conv_1x1_resident_kernel(const ConvArg
   constexpr int MB = RES_MB, NB = RES_NB, BM = RES_BM, BN = RES_BN;
   constexpr int STAGE = (BM + BN) * KC;       // one K step: activation rows, then weight rows
   constexpr int ACH = BM / 8, BCH = BN / 8;   // 1 KB chunks (8 rows x 128 B) per K step
-  constexpr int ALOADS = (KS * ACH + 7) / 8, BLOADS = (KS * BCH + 7) / 8;  // per wavefront
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[KS * STAGE];
+  // one array per K step: the compiler tracks LDS-DMA writes per array, so a step's fragment reads wait only for the
+  // loads into that step (one array for all would make every read wait for every load in flight)
+  __shared__ __attribute__((aligned(1024))) uint8_t stage0[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t stage1[KS > 1 ? STAGE : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t stage2[KS > 2 ? STAGE : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t stage3[KS > 3 ? STAGE : 16];
+  auto stage_of = [&](int st) __attribute__((always_inline)) -> uint8_t* {
+    return st == 0 ? stage0 : st == 1 ? stage1 : st == 2 ? stage2 : stage3;
+  };
   __shared__ __attribute__((aligned(16))) float ep_scale[BN], ep_bias[BN], ep_osc[BN];
 
   const int tid = threadIdx.x;
@@ -1877,16 +1884,38 @@ __global__ __launch_bounds__(512, 1) void conv_1x1_resident_kernel(const ConvArg
   if (first >= total) return;
   const int n0 = (first % a.n_tiles) * BN;
 
-  if (tid < BN) {
-    const int n = n0 + tid;
-    const bool nok = n < a.Cout;
-    ep_scale[tid] = (KIND == KIND_INT8 && nok) ? *a.a_scale * a.w_scale[n] : 1.0f;
-    float bias = -0.0f;
-    if (a.bias != nullptr && nok)
-      bias = a.bias_dtype == FIM_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(a.bias)[n])
-                                      : static_cast<const float*>(a.bias)[n];
-    ep_bias[tid] = bias;
-    ep_osc[tid] = (OUT == OUT_E4M3 && nok) ? exp2_int((int)a.out_expo[n >> 5]) : 1.0f;
+  // Prologue: every load is issued without a branch (small operands by range-checked buffer loads, out-of-range and
+  // absent operands reading as zero; the operand chunks unconditional), so the compiler counts them exactly and its
+  // waits for the small operands do not wait for the operand chunks issued after them.
+  const int n_ep = min(n0 + tid, a.Cout - 1);  // lanes >= BN compute a value nobody stores
+  float ep_s = 1.0f, ep_b, ep_o = 1.0f;
+  {
+    const bool bf = a.bias_dtype == FIM_BF16, has = a.bias != nullptr;
+    const int esz = bf ? 2 : 4;
+    const void* bp = has ? a.bias : static_cast<const void*>(fim_zero_segment);
+    const __amdgpu_buffer_rsrc_t br =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(bp), (short)0, has ? a.Cout * esz : 0, 0x00020000);
+    // two 16-bit loads (the high one reads past a BF16 bias's last element as zero): both always issued, so no
+    // branch; the value is selected afterwards
+    const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(br, n_ep * esz, 0, 0);
+    const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(br, n_ep * esz + 2, 0, 0);
+    const uint32_t lsh = bf ? 16u : 0u, hmask = bf ? 0u : 0xffffffffu;  // arithmetic, so both loads are always used
+    const uint32_t bits = (lo << lsh) | ((hi << 16) & hmask);
+    ep_b = has ? __builtin_bit_cast(float, bits) : -0.0f;  // -0: x + (-0) == x
+    if constexpr (KIND == KIND_INT8) {
+      const float as = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.a_scale), (short)0, 4, 0x00020000), 0, 0, 0));
+      const float ws = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.w_scale), (short)0, a.Cout * 4, 0x00020000),
+          n_ep * 4, 0, 0));
+      ep_s = as * ws;
+    }
+    if constexpr (OUT == OUT_E4M3) {
+      const int8_t oe = (int8_t)__builtin_amdgcn_raw_buffer_load_b8(
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(a.out_expo), (short)0, (a.Cout + 31) >> 5, 0x00020000),
+          n_ep >> 5, 0, 0);
+      ep_o = exp2_int((int)oe);
+    }
   }
 
   const int x_nrec = __builtin_amdgcn_readfirstlane((int)((int64_t)a.M * a.Cin));
@@ -1895,40 +1924,72 @@ __global__ __launch_bounds__(512, 1) void conv_1x1_resident_kernel(const ConvArg
   // lane's row within a chunk and the global segment it fetches (slot lane % 8 holds segment (lane % 8) ^ ((r / 2) % 8))
   const int crow = lane >> 3;
 
-  // all K steps of tile t's activation rows (rows past M read as zero)
-  auto load_a = [&](int t) __attribute__((always_inline)) {
-    const int m0 = (t / a.n_tiles) * BM;
+  // MXFP8 scales per K step: the lane's activation block 4 st + g and its weight rows' bytes of that block
+  int sx[KS], sw[KS][NB];
+  if constexpr (KIND == KIND_MX) {
+    const int cblocks = a.Cin >> 5;
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(a.x_expo), (short)0, cblocks, 0x00020000);
+    const __amdgpu_buffer_rsrc_t wr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(a.w_expo), (short)0, a.Cout * cblocks, 0x00020000);
 #pragma unroll
-    for (int i = 0; i < ALOADS; ++i) {
-      const int k = wave + 8 * i;
-      if (k < KS * ACH) {  // uniform
-        const int st = k / ACH, c = k % ACH;
-        const int r = 8 * c + crow;
-        const int seg = (lane & 7) ^ ((r >> 1) & 7);
-        const int m = m0 + r;
-        const uint32_t off = m < a.M ? (uint32_t)(m * a.Cin + st * KC + seg * 16) : OOB;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.x), (short)0, x_nrec, 0x00020000),
-            (lds_void_t*)(smem + st * STAGE + c * 1024), 16, off, 0, 0, 0);
+    for (int st = 0; st < KS; ++st) {
+      sx[st] = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(xr, 4 * st + g, 0, 0) + 127;
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const int n = min(n0 + wn * (NB * 16) + i * 16 + (lane & 15), a.Cout - 1);
+        sw[st][i] = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(wr, n * cblocks + 4 * st + g, 0, 0) + 127;
       }
     }
-  };
-  // the block's weight rows, every K step (channels past Cout read as zero)
+  }
+
+  asm volatile("" ::: "memory");  // the small loads stay ahead of the operand loads (the compiler would sink them)
+
+  // K step st of tile t's activation rows (rows past M read as zero): chunks wave + 8 i of the step's ACH; where that
+  // is past ACH, the wavefront loads its chunk of the previous i again (the same bytes to the same place), so every
+  // wavefront issues the same number of loads and no branch
+  constexpr int NA = (ACH + 7) / 8, NW = (BCH + 7) / 8;
+  auto load_a_step = [&](int t, int st) __attribute__((always_inline)) {
+    const int m0 = (t / a.n_tiles) * BM;
 #pragma unroll
-  for (int i = 0; i < BLOADS; ++i) {
-    const int k = wave + 8 * i;
-    if (k < KS * BCH) {
-      const int st = k / BCH, c = k % BCH;
+    for (int i = 0; i < NA; ++i) {
+      const int c = wave + 8 * i < ACH ? wave + 8 * i : wave + 8 * i - 8;
+      const int r = 8 * c + crow;
+      const int seg = (lane & 7) ^ ((r >> 1) & 7);
+      const int m = m0 + r;
+      const uint32_t off = m < a.M ? (uint32_t)(m * a.Cin + st * KC + seg * 16) : OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.x), (short)0, x_nrec, 0x00020000),
+          (lds_void_t*)(stage_of(st) + c * 1024), 16, off, 0, 0, 0);
+    }
+  };
+  // K step st of the block's weight rows (channels past Cout read as zero)
+  auto load_w_step = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      const int c = wave + 8 * i < BCH ? wave + 8 * i : wave + 8 * i - 8;
       const int r = BM + 8 * c + crow;  // LDS row
       const int seg = (lane & 7) ^ ((r >> 1) & 7);
       const int n = n0 + r - BM;
       const uint32_t off = n < a.Cout ? (uint32_t)(n * a.Cin + st * KC + seg * 16) : OOB;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), (short)0, w_nrec, 0x00020000),
-          (lds_void_t*)(smem + st * STAGE + (ACH + c) * 1024), 16, off, 0, 0, 0);
+          (lds_void_t*)(stage_of(st) + (ACH + c) * 1024), 16, off, 0, 0, 0);
     }
+  };
+  // the first tile step by step, each step's weights and activations together: its K loop starts once step 0 landed
+  // and waits for each further step as it reaches it, instead of for all of them
+#pragma unroll
+  for (int st = 0; st < KS; ++st) {
+    load_w_step(st);
+    load_a_step(first, st);
   }
-  load_a(first);
+  constexpr int PER_STEP = NA + NW;  // loads per step of every wavefront
+  if (tid < BN) {
+    ep_scale[tid] = ep_s;
+    ep_bias[tid] = ep_b;
+    ep_osc[tid] = ep_o;
+  }
 
   // fragment offsets within a K step (the conv stages' layout: lo half at f, hi half at f ^ 64)
   int fr_x[MB], fr_w[NB];
@@ -1942,22 +2003,7 @@ __global__ __launch_bounds__(512, 1) void conv_1x1_resident_kernel(const ConvArg
     const int r = BM + wn * (NB * 16) + i * 16 + (lane & 15);
     fr_w[i] = r * KC + ((g ^ ((r >> 1) & 7)) << 4);
   }
-  // MXFP8 scales per K step: the lane's activation block 4 st + g and its weight rows' bytes of that block
-  int sx[KS], sw[KS][NB];
-  if constexpr (KIND == KIND_MX) {
-    const int cblocks = a.Cin >> 5;
-#pragma unroll
-    for (int st = 0; st < KS; ++st) {
-      sx[st] = (int)a.x_expo[4 * st + g] + 127;
-#pragma unroll
-      for (int i = 0; i < NB; ++i) {
-        const int n = n0 + wn * (NB * 16) + i * 16 + (lane & 15);
-        sw[st][i] = (int)a.w_expo[(int64_t)(n < a.Cout ? n : 0) * cblocks + 4 * st + g] + 127;
-      }
-    }
-  }
 
-  vm_lds_barrier();  // weights and the first tile landed
   for (int t = first; t < total; t += stride) {
     v4i acc_i[NB][MB];
     v4f acc_f[NB][MB];
@@ -1970,7 +2016,11 @@ __global__ __launch_bounds__(512, 1) void conv_1x1_resident_kernel(const ConvArg
       }
 #pragma unroll
     for (int st = 0; st < KS; ++st) {
-      const uint8_t* cur = smem + st * STAGE;
+      if (t == first) {  // step st of the first tile (and, at step 0, the staged epilogue operands) landed everywhere
+        wait_vm_at_most((KS - 1 - st) * PER_STEP);
+        asm volatile("s_barrier" ::: "memory");
+      }
+      const uint8_t* cur = stage_of(st);
       v8i xf[MB], wf[NB];
 #pragma unroll
       for (int j = 0; j < MB; ++j) {
@@ -2013,7 +2063,10 @@ __global__ __launch_bounds__(512, 1) void conv_1x1_resident_kernel(const ConvArg
       }
     lds_barrier();  // every wavefront has read this tile's activations
     const int next = t + stride;
-    if (next < total) load_a(next);
+    if (next < total) {
+#pragma unroll
+      for (int st = 0; st < KS; ++st) load_a_step(next, st);
+    }
     conv_epilogue<KIND, OUT, 0, MB, NB>(a, acc_i, acc_f, (t / a.n_tiles) * BM + wm * (MB * 16), n0, wn * (NB * 16),
                                         ep_scale, ep_bias, ep_osc);
     if (next < total) vm_lds_barrier();  // the next tile's activations landed

@@ -46,7 +46,7 @@ struct Quantizer {
     if (gelu) {
       if (in_bias != nullptr) v = __fadd_rn(v, in_bias[c]);
       v = gelu == 2 ? gelu_tanh(v) : gelu_erf(v);
-      if (rnd == FIM_BF16) v = round_bf16(v);
+      if (rnd == FIM_BF16) v = round_bf16_hw(v);
       else if (rnd == FIM_F16) v = (float)(_Float16)v;
     }
     if (MODE == MODE_INT8) {

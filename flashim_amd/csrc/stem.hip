@@ -43,7 +43,7 @@ struct StemArgs {
 // FP32 promotes). The ReLU that follows is folded into the quantizer's saturation.
 __device__ __forceinline__ float bias_add(float v, float b, bool bias_bf16) {
   const float t = __fadd_rn(v, b);
-  return bias_bf16 ? round_bf16(t) : t;
+  return bias_bf16 ? round_bf16_hw(t) : t;
 }
 
 template <int NCH, int CHUNKS>  // Cout / 16; KP / 32
