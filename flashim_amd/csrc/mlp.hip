@@ -139,88 +139,99 @@ __global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
     load_res(t + gridDim.x, res_nxt);
 
     // ---- expand: wave w computes hidden channels [64 w, 64 w + 64) x all 64 pixels ----------------------------
-    // all 16 MFMAs first (their latency then hides behind each other), the VALU-heavy epilogues after
+    // 32 x 32 MFMA blocks (2 hidden x 2 pixel blocks per wave): MXFP8 v_mfma_scale_f32_32x32x64_f8f6f4 takes the
+    // whole K = 64 in one instruction (no zero-padded K half), INT8 two v_mfma_i32_32x32x32_i8. Operand layout
+    // (measured on gfx950): lane l supplies row l % 32; for the scaled MFMA, bytes 0-15 are K [16 h, 16 h + 16) and
+    // bytes 16-31 are K [32 + 16 h, +16) with h = l / 32, and the scale of lane i + 32 kb covers K block kb of row i;
+    // the INT8 products are exact, so any K order shared by both operands gives the same int32 sums. Output: register r
+    // of lane l is row 8 (r / 4) + 4 h + r % 4, column l % 32: a lane holds 4 groups of 4 consecutive hidden channels
+    // of one pixel, all in one 32-channel scale block. All MFMAs first (their latency hides behind each other), the
+    // VALU-heavy epilogues after.
     {
-      v4i xf[4];
+      const int l32 = lane & 31, h2 = lane >> 5;
+      v4i xlo[2], xhi[2];  // pixel rows 32 jb + l32: 16-byte slots h2 and 2 + h2
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int row = 16 * j + r16;
-        xf[j] = *reinterpret_cast<const v4i*>(&xs[row * MLP_C + ((g ^ ((row >> 2) & 3)) << 4)]);
+      for (int jb = 0; jb < 2; ++jb) {
+        const int row = 32 * jb + l32;
+        xlo[jb] = *reinterpret_cast<const v4i*>(&xs[row * MLP_C + ((h2 ^ ((row >> 2) & 3)) << 4)]);
+        xhi[jb] = *reinterpret_cast<const v4i*>(&xs[row * MLP_C + (((2 + h2) ^ ((row >> 2) & 3)) << 4)]);
       }
-      // lane group g scales K block g; blocks 2, 3 are the zero hi half (scale 2^0). Unconditional reads from a
-      // clamped index, then selects: no divergent branches.
-      const int sx = g == 0 ? xe[0] + 127 : g == 1 ? xe[1] + 127 : 127;
-      v4i acc_i[4][4];
-      v4f acc_f[4][4];
+      v16i acc_i[2][2];
+      v16f acc_f[2][2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int h = 64 * wave + 16 * i + r16;
-        const v4i wf = *reinterpret_cast<const v4i*>(&w1s[h * MLP_C + ((g ^ ((h >> 2) & 3)) << 4)]);
-        const int e = e1s[2 * h + (g & 1)];
-        const int sw = g < 2 ? e + 127 : 127;
+      for (int ib = 0; ib < 2; ++ib) {
+        const int h = 64 * wave + 32 * ib + l32;
+        const v4i wlo = *reinterpret_cast<const v4i*>(&w1s[h * MLP_C + ((h2 ^ ((h >> 2) & 3)) << 4)]);
+        const v4i whi = *reinterpret_cast<const v4i*>(&w1s[h * MLP_C + (((2 + h2) ^ ((h >> 2) & 3)) << 4)]);
+        const int sw = (int)e1s[2 * h + h2] + 127;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int jb = 0; jb < 2; ++jb) {
           if (KIND == MLP_INT8) {
-            acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf, xf[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+            v16i c = {};
+            c = __builtin_amdgcn_mfma_i32_32x32x32_i8(wlo, xlo[jb], c, 0, 0, 0);
+            acc_i[ib][jb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(whi, xhi[jb], c, 0, 0, 0);
           } else {
-            const v8i wa = v8i{wf[0], wf[1], wf[2], wf[3], 0, 0, 0, 0};
-            const v8i xb = v8i{xf[j][0], xf[j][1], xf[j][2], xf[j][3], 0, 0, 0, 0};
-            acc_f[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wa, xb, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0,
-                                                                           sw, 0, sx);
+            const v8i wa = __builtin_shufflevector(wlo, whi, 0, 1, 2, 3, 4, 5, 6, 7);
+            const v8i xb = __builtin_shufflevector(xlo[jb], xhi[jb], 0, 1, 2, 3, 4, 5, 6, 7);
+            acc_f[ib][jb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wa, xb, v16f{}, 0, 0, 0, sw, 0,
+                                                                            xe[h2] + 127);
           }
         }
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int h0 = 64 * wave + 16 * i + 4 * g;  // this lane's 4 output channels
-        float yb[4][4];  // the block's 16 values, all computed before any is quantized (one INT8 tie test)
+      for (int ib = 0; ib < 2; ++ib) {
+        const int hb = 64 * wave + 32 * ib + 4 * h2;  // hidden channel of register 0; register r adds 8 (r / 4) + r % 4
+        // MXFP8: the block's scale; GELU outputs are >= -0.1700 (BF16), so the lower clamp at -448 * 2^e is a no-op
+        // for every scale >= 2^-11 (wave-uniform: the wave's 32 channels share one scale block)
+        const float sc = KIND == MLP_MX ? hsc[hb] : 1.0f, bound = 448.0f * sc;
+        const bool two_sided = __builtin_amdgcn_readfirstlane((int)(sc < 0x1p-11f)) != 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float (&y)[4] = yb[j];
-          if (KIND == MLP_INT8) {
+        for (int jb = 0; jb < 2; ++jb) {
+          float yb[16];  // the block's 16 values, all computed before any is quantized (one INT8 tie test)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) y[v] = __fadd_rn(__fmul_rn((float)acc_i[i][j][v], s1[h0 + v]), b1s[h0 + v]);
-          } else if (SEM == MLP_REFERENCE) {  // bf16(x W1^T), + b1 in FP32, GELU of the FP32 sum
+          for (int r = 0; r < 16; ++r) {
+            const int hh = hb + 8 * (r >> 2) + (r & 3);
+            float y;
+            if (KIND == MLP_INT8) {
+              y = __fadd_rn(__fmul_rn((float)acc_i[ib][jb][r], s1[hh]), b1s[hh]);
+            } else if (SEM == MLP_REFERENCE) {  // bf16(x W1^T), + b1 in FP32, GELU of the FP32 sum
+              y = __fadd_rn(round_bf16_hw(acc_f[ib][jb][r]), b1s[hh]);
+            } else {
+              y = __fadd_rn(acc_f[ib][jb][r], b1s[hh]);
+            }
+            yb[r] = SEM == MLP_BLOCK ? round_bf16_hw(y) : y;  // the conv epilogue: BF16 rounding before the GELU
+          }
+          gelu_erf_n<16>(yb);  // the block's 16 GELU chains interleaved
+          uint32_t qw[4];
+          if (KIND == MLP_MX) {  // BF16 rounding and static E4M3 in one step
 #pragma unroll
-            for (int v = 0; v < 4; ++v) y[v] = acc_f[i][j][v];
-            round_bf16x2(y[0], y[1]);
-            round_bf16x2(y[2], y[3]);
+            for (int k = 0; k < 4; ++k) {
+              float q[4];
 #pragma unroll
-            for (int v = 0; v < 4; ++v) y[v] = __fadd_rn(y[v], b1s[h0 + v]);
+              for (int v = 0; v < 4; ++v) q[v] = __builtin_elementwise_minimum(yb[4 * k + v], bound);
+              if (two_sided) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) q[v] = __builtin_elementwise_maximum(q[v], -bound);
+              }
+              qw[k] = e4m3x4_of_bf16_inrange(q[0], q[1], q[2], q[3], sc);
+            }
           } else {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) y[v] = __fadd_rn(acc_f[i][j][v], b1s[h0 + v]);
+            for (int r = 0; r < 16; ++r) yb[r] = round_bf16_hw(yb[r]);
+            int qi[16];
+            quantize_int8_fast_n<16>(yb, hq_scale, hq_inv, qi);
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+              qw[k] = (uint32_t)(uint8_t)qi[4 * k] | ((uint32_t)(uint8_t)qi[4 * k + 1] << 8) |
+                      ((uint32_t)(uint8_t)qi[4 * k + 2] << 16) | ((uint32_t)(uint8_t)qi[4 * k + 3] << 24);
           }
-          if (SEM == MLP_BLOCK) {  // the conv epilogue: BF16 rounding before the GELU
-            round_bf16x2(y[0], y[1]);
-            round_bf16x2(y[2], y[3]);
+          const int px = 32 * jb + l32;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int h0 = hb + 8 * k;
+            *reinterpret_cast<uint32_t*>(&hs[px * MLP_H + ((((h0 >> 4)) ^ (px & 15)) << 4) + (h0 & 15)]) = qw[k];
           }
-        }
-        gelu_erf_n<16>(reinterpret_cast<float (&)[16]>(yb));  // the block's 16 GELU chains interleaved
-        uint32_t qw[4];
-        if (KIND == MLP_MX) {  // BF16 rounding and static E4M3 in one step (the lane's 4 channels share a scale block)
-          const float sc = hsc[h0], bound = 448.0f * sc;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) qw[j] = e4m3x4_of_bf16(yb[j][0], yb[j][1], yb[j][2], yb[j][3], sc, bound);
-        } else {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            round_bf16x2(yb[j][0], yb[j][1]);
-            round_bf16x2(yb[j][2], yb[j][3]);
-          }
-          const float (&flat)[16] = reinterpret_cast<const float (&)[16]>(yb);
-          int qi[16];
-          quantize_int8_fast_n<16>(flat, hq_scale, hq_inv, qi);
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            qw[j] = (uint32_t)(uint8_t)qi[4 * j] | ((uint32_t)(uint8_t)qi[4 * j + 1] << 8) |
-                    ((uint32_t)(uint8_t)qi[4 * j + 2] << 16) | ((uint32_t)(uint8_t)qi[4 * j + 3] << 24);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int px = 16 * j + r16;
-          *reinterpret_cast<uint32_t*>(&hs[px * MLP_H + ((((h0 >> 4)) ^ (px & 15)) << 4) + (h0 & 15)]) = qw[j];
         }
       }
     }
