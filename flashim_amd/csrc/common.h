@@ -100,31 +100,32 @@ __device__ __forceinline__ uint8_t e4m3(float a) {
 }
 
 // GELU, erf form: 0.5 x erfc(-x / sqrt 2) = max(x, 0) - |x| E with E = erfc(|x| / sqrt 2) / 2 (x >= 0: x - x E;
-// x < 0: x E). With t = 2 |x| / 4 - 1, log2 E is the degree-5 polynomial P(t) below (a near-minimax fit of
-// log2(erfc(|x| / sqrt 2) / 2) for |x| in [0, 4], this repository's own, max error 7.2e-5 in log2 units, i.e. 5e-5
-// relative in E), so E = 2^P(t): one v_exp_f32, 5 FMAs, no division, and the last step is one FMA,
-// fma(-|x|, E, max(x, -0)). Beyond the fit E < 3.2e-5, where its error no longer reaches a BF16 result: the positive
-// side is x (1 - E) with E far below half a BF16 step, and the negative side is smaller than 1.3e-4 in magnitude (a
-// fit to |x| = 3.5 only measured more E4M3 code differences from torch in that tail at tiny static scales). The polynomial needs no clamp: its leading coefficient is negative and P decreases
-// monotonically for t > 1 (-14.9 at the fit's end, below -700 at |x| = 20, -inf once its leading term overflows), so
-// the large-|x| limits come out right by themselves: x - 0 = x for large positive x, and -0 (fma(-|x|, 0, -0)) once
-// 2^P underflows for large negative x. Between x = -5.53 (where torch's FP32 1 + erf(x / sqrt 2) becomes exactly 0, so
-// torch returns -0) and the underflow the result is a tiny negative value instead of -0. Against torch's BF16 GELU it
-// differs by one BF16 step in about 1% of the finite BF16 inputs (torch's own erf rounding moves values across BF16
-// rounding boundaries too; the degree-8 and degree-7 fits this replaced differed on the same fraction); in torch's
-// cancelling negative tail (x < -3) both are within 2^-12 of each other. Signed zeros follow torch: GELU(+0) = +0,
-// GELU(-0) = -0. Evaluated in the rescaled variable u = s t, s = |c5|^(1/5) = 0.40947369, where the polynomial is
-// monic up to sign (coefficients c_k / s^k): its first Horner step is one subtraction with one literal, and
-// u = |x| 2 s / 4 - s is one FMA.
-constexpr float kGeluS = 0.40947369f, kGeluU = 0.20473684f;  // s, 2 s / 4
-constexpr float kGeluC0 = 1.4789375f;                        // c4 / s^4 (the first Horner step: kGeluC0 - u)
-constexpr float kGeluC[4] = {-1.6612425f, -15.250149f, -16.723097f,
-                             -5.4579101f};  // c3 / s^3 .. c0 (c0 includes the -1 of the factor 1/2)
+// x < 0: x E). With z = |x| / sqrt 2 and t = 2 z / 4.1 - 1, log2 E is the degree-7 polynomial P(t) below (a near-minimax
+// fit of log2(erfc(z) / 2) on [0, 4.1], this repository's own, max error 4.7e-6 in log2 units, i.e. 3.3e-6 relative in
+// E), so E = 2^P(t): one v_exp_f32, 7 FMAs, no division, and the last step is one FMA, fma(-|x|, E, max(x, -0)). The
+// polynomial needs no clamp outside the fit: its leading coefficient is negative and P decreases monotonically for
+// t > 1 (P = -28.2 at the fit's end, below -900 at |x| = 40, -inf once its leading term overflows), so the large-|x|
+// limits come out right by themselves: x - 0 = x for large positive x, and -0 (fma(-|x|, 0, -0)) once 2^P underflows for
+// large negative x. Between x = -5.53 (where torch's FP32 1 + erf(x / sqrt 2) becomes exactly 0, so torch returns -0)
+// and about x = -12 the result is the true tiny GELU value (< 1e-7 in magnitude) instead of -0. Against torch's BF16
+// GELU it differs by one BF16 step in about 1% of the finite BF16 inputs (torch's own erf rounding moves values across
+// BF16 rounding boundaries too); in torch's cancelling negative tail (x < -3) both are within 2^-12 of each other.
+// Signed zeros follow torch: GELU(+0) = +0, GELU(-0) = -0. A degree-5 fit (two FMAs fewer, 5e-5 relative) was measured
+// too: the same fraction of one-step differences over all BF16 inputs, but true values within 5e-5 of a BF16 rounding
+// midpoint then round to the other side of it far more often (7.7% of one INT8 linear's GELU outputs against torch),
+// so the more accurate fit stays.
+// Evaluated in the rescaled variable u = s t, s = |c7|^(1/7) = 0.43911893, where the polynomial is monic up to sign
+// (coefficients c_k / s^k): its first Horner step is one subtraction with one literal, and u = |x| s sqrt(2) / 4.1 - s
+// is one FMA.
+constexpr float kGeluS = 0.43911893f, kGeluU = 0.15146535f;  // s, s sqrt(2) / 4.1
+constexpr float kGeluC0 = 2.019375f;                         // c6 / s^6 (the first Horner step: kGeluC0 - u)
+constexpr float kGeluC[6] = {-2.2946658f, 2.3185021f, -2.3095699f, -29.120948f, -30.379971f,
+                             -9.0620125f};  // c5 / s^5 .. c0 (c0 includes the -1 of the factor 1/2)
 __device__ __forceinline__ float gelu_erf(float x) {
   const float u = fmaf(fabsf(x), kGeluU, -kGeluS);
-  float p = kGeluC0 - u;  // -u^5 + (c4 / s^4) u^4: the first Horner step
+  float p = kGeluC0 - u;  // -u^7 + (c6 / s^6) u^6: the first Horner step
 #pragma unroll
-  for (int k = 0; k < 4; ++k) p = fmaf(p, u, kGeluC[k]);
+  for (int k = 0; k < 6; ++k) p = fmaf(p, u, kGeluC[k]);
   return fmaf(-fabsf(x), __builtin_amdgcn_exp2f(p), __builtin_elementwise_maximum(x, -0.0f));
 }
 
@@ -151,7 +152,7 @@ __device__ __forceinline__ void gelu_erf_n(float (&x)[N]) {
 #pragma unroll
   for (int i = 0; i < N; ++i) p[i] = kGeluC0 - u[i];
 #pragma unroll
-  for (int k = 0; k < 4; ++k)
+  for (int k = 0; k < 6; ++k)
 #pragma unroll
     for (int i = 0; i < N; ++i) p[i] = fmaf(p[i], u[i], kGeluC[k]);
 #pragma unroll
