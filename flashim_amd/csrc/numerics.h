@@ -165,31 +165,37 @@ FIM_HD int8_t quantize_int8_value(float x, float scale) {
 #ifdef __HIPCC__
 // quantize_int8_value with the division replaced by a multiply by inv = 1 / scale (correctly rounded), falling back
 // to the IEEE division only where it can matter: x * inv is within a few ulps of the exact quotient, so both round to
-// the same integer unless the quotient sits within 2^-15 of a half-integer, i.e. |t - rint(t)| >= 0.5 - 2^-15 for
-// t = x * inv (t - rint(t) is exact); beyond |q| = 127 both saturate. The fallback sits behind one wave-uniform branch
-// for all N values (taken when any lane is near a tie), so it neither runs per element nor splits the code that
-// produces the inputs. The saturation is one v_med3_f32 (LO = 0 folds a preceding ReLU in: relu then quantize equals
-// clamping the rounded quotient at 0). Checked on the host against round(x / s) on 20M cases including exact ties and
-// their neighbours, with and without the ReLU.
+// the same integer unless the quotient sits within 2^-15 of a half-integer; beyond |q| = 127 both saturate. The
+// rounding is one FMA with M = 1.5 * 2^23: fma(x, inv, M) rounds x * inv + M once, to the nearest integer (ties to
+// even) on the grid of unit spacing where M sits, so its low mantissa bits hold rint(x * inv) and its low byte is the
+// INT8 code in two's complement; r = f - M (exact) is the rounded quotient and fma(x, inv, -r) the exact residual, and
+// |residual| >= 0.5 - 2^-15 marks a near-tie. The fallback sits behind one wave-uniform branch for all N values (taken
+// when any lane is near a tie), so it neither runs per element nor splits the code that produces the inputs. The
+// saturation is one v_med3_f32 between M - 127 and M + 127 (LO = 0 folds a preceding ReLU in: relu then quantize
+// equals clamping the rounded quotient at 0), so no conversion to an integer is needed: q[i] holds the clamped value's
+// bit pattern, whose low byte is the code (callers keep that byte). 5 VALU operations per value. Checked on the host
+// against round(x / s) on 20M cases including exact ties and their neighbours, with and without the ReLU, and on the
+// GPU byte for byte against the torch references of every INT8 producer.
 template <int N, int LO = -127>
 __device__ __forceinline__ void quantize_int8_fast_n(const float (&x)[N], float scale, float inv, int (&q)[N]) {
-  float r[N];
+  constexpr float M = 12582912.0f;  // 1.5 * 2^23
+  float f[N];
   bool near[N];
   bool any = false;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    const float t = x[i] * inv;
-    r[i] = __builtin_rintf(t);
-    near[i] = fabsf(t - r[i]) >= 0.5f - 0x1p-15f;
+    f[i] = fmaf(x[i], inv, M);
+    const float r = f[i] - M;
+    near[i] = fabsf(fmaf(x[i], inv, -r)) >= 0.5f - 0x1p-15f;
     any = any || near[i];
   }
   if (__builtin_amdgcn_ballot_w64(any) != 0) {
 #pragma unroll
     for (int i = 0; i < N; ++i)
-      if (near[i]) r[i] = __builtin_rintf(__fdiv_rn(x[i], scale));
+      if (near[i]) f[i] = __builtin_rintf(__fdiv_rn(x[i], scale)) + M;
   }
 #pragma unroll
-  for (int i = 0; i < N; ++i) q[i] = (int)__builtin_amdgcn_fmed3f(r[i], (float)LO, 127.0f);
+  for (int i = 0; i < N; ++i) q[i] = __builtin_bit_cast(int, __builtin_amdgcn_fmed3f(f[i], M + (float)LO, M + 127.0f));
 }
 
 __device__ __forceinline__ int8_t quantize_int8_fast(float x, float scale, float inv) {
