@@ -99,6 +99,18 @@ __device__ __forceinline__ uint8_t e4m3(float a) {
   return (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(a, a, 0, false) & 0xff);
 }
 
+// mx_exponent_from_amax for a finite amax >= 0 in wave-uniform control flow: the division-free mx_exponent_fast, and
+// the exact path behind one wave-uniform branch for the lanes it declines (all-zero blocks, quotients near a power of
+// two).
+__device__ __forceinline__ int mx_exponent_wave(float amax) {
+  int e = 0;
+  const bool fast = mx_exponent_fast(amax, e);
+  if (__builtin_amdgcn_ballot_w64(!fast) != 0) {
+    if (!fast) e = mx_exponent_from_amax(amax);
+  }
+  return e;
+}
+
 // GELU, erf form: 0.5 x erfc(-x / sqrt 2) = max(x, 0) - |x| E with E = erfc(|x| / sqrt 2) / 2 (x >= 0: x - x E;
 // x < 0: x E). With z = |x| / sqrt 2 and t = 2 z / 4.1 - 1, log2 E is the degree-7 polynomial P(t) below (a near-minimax
 // fit of log2(erfc(z) / 2) on [0, 4.1], this repository's own, max error 4.7e-6 in log2 units, i.e. 3.3e-6 relative in

@@ -210,7 +210,13 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
         for (int i = 0; i < 4; ++i) y[t][cq][i] = fmaxf(acc[t][cq][i], 0.f);
     const int64_t groups = a.C >> 5;
     const int64_t tiles_k = (groups + 3) >> 2;
+    const int64_t gi = cbase >> 5;
     float* st = reinterpret_cast<float*>(sm);
+    // output pass lanes: 4 consecutive lanes share a pixel (part = 8-channel quarter of the slice); unit tid + 256 it
+    // is tile row 2 it + (tid >> 7) of the half, column (tid >> 2) & 31, so addresses advance by a uniform step per it
+    const int part = tid & 3, col = (tid >> 2) & 31, rl0 = tid >> 7;
+    const int64_t row0 = ((int64_t)b * a.H + y0 + rl0) * a.W + x0 + col;  // output pixel of it = 0, half 0
+    uint8_t* const out0 = static_cast<uint8_t*>(a.out) + row0 * a.C + cbase + 8 * part;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       __syncthreads();  // half 0: the taps are done with the input tile; half 1: the previous output pass is done
@@ -224,12 +230,10 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
               st[(4 * t + r4) * DWM_OROW + (4 * cq + i) * DW_CS + 16 * cg + bch] = y[t][cq][i];
       }
       __syncthreads();
-      // output pass: 8 rows x 32 columns x 4 parts of 8 channels; 4 consecutive lanes share a pixel
+      // output pass: 8 rows x 32 columns x 4 parts of 8 channels
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
-        const int unit = tid + 256 * it;
-        const int part = unit & 3, px = unit >> 2;  // px: 8 rows x 32 columns
-        const int rl = px >> 5, col = px & 31;
+        const int rl = rl0 + 2 * it;
         const int oy = 8 * half + rl;
         const float4 va = *reinterpret_cast<const float4*>(&st[rl * DWM_OROW + col * DW_CS + 8 * part]);
         const float4 vb = *reinterpret_cast<const float4*>(&st[rl * DWM_OROW + col * DW_CS + 8 * part + 4]);
@@ -238,18 +242,18 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
         float amax = fmaxf(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])), fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7])));
         amax = fmaxf(amax, __shfl_xor(amax, 1));
         amax = fmaxf(amax, __shfl_xor(amax, 2));
-        const int ex = mx_exponent_from_amax(amax);
+        const int ex = mx_exponent_wave(amax);
         const float inv = exp2_int(-ex);
         float q[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) q[e] = __builtin_elementwise_minimum(v[e] * inv, 448.0f);
         const bool ok = interior || (oy < rows && col < cols);
         if (ok) {
-          const int64_t row = ((int64_t)b * a.H + y0 + oy) * a.W + x0 + col;
-          *reinterpret_cast<uint2*>(static_cast<uint8_t*>(a.out) + row * a.C + cbase + 8 * part) =
+          const int64_t step = (int64_t)(8 * half + 2 * it) * a.W;  // uniform
+          *reinterpret_cast<uint2*>(out0 + step * a.C) =
               make_uint2(pack_e4m3x4(q[0], q[1], q[2], q[3]), pack_e4m3x4(q[4], q[5], q[6], q[7]));
           if (part == 0) {
-            const int64_t gi = cbase >> 5;
+            const int64_t row = row0 + step;
             if (a.expo_out != nullptr) a.expo_out[row * groups + gi] = (int8_t)ex;
             if (a.swizzled != nullptr) {
               const int64_t rt = row & 127;

@@ -172,17 +172,16 @@ __global__ __launch_bounds__(256, 2) void dw_pw_kernel(const DwPwArgs a) {
         float v[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
         uint2 codes;
         const int p = (4 * half + rl) * DP_TW + col;  // tile pixel
-        float amax = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+        // the values are >= 0 (ReLU): the amax is a plain max and the clamp is one-sided
+        float amax = fmaxf(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])), fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7])));
         amax = fmaxf(amax, __shfl_xor(amax, 1));
         amax = fmaxf(amax, __shfl_xor(amax, 2));
-        const int ex = mx_exponent_from_amax(amax);
+        const int ex = mx_exponent_wave(amax);
         const float inv = exp2_int(-ex);
-        codes = make_uint2(pack_e4m3x4(mx_scale_clamp(v[0], inv), mx_scale_clamp(v[1], inv),
-                                       mx_scale_clamp(v[2], inv), mx_scale_clamp(v[3], inv)),
-                           pack_e4m3x4(mx_scale_clamp(v[4], inv), mx_scale_clamp(v[5], inv),
-                                       mx_scale_clamp(v[6], inv), mx_scale_clamp(v[7], inv)));
+        float q[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q[e] = __builtin_elementwise_minimum(v[e] * inv, 448.0f);
+        codes = make_uint2(pack_e4m3x4(q[0], q[1], q[2], q[3]), pack_e4m3x4(q[4], q[5], q[6], q[7]));
         if (part == 0) aexp[p * 4 + s] = (int8_t)ex;
         const int seg = 2 * s + (part >> 1);  // 16-byte slot of channels [32 s + 8 part, + 8)
         *reinterpret_cast<uint2*>(&act[p * DP_C + ((seg ^ ((p >> 1) & 7)) << 4) + 8 * (part & 1)]) = codes;

@@ -149,6 +149,19 @@ FIM_HD int mx_exponent_from_amax(float amax) {
   return e;
 }
 
+// The same exponent without the division, for a finite amax >= 0, when it can be decided from q' = amax * RN(1/448):
+// q' is within 2 units in the last place of q = RN(amax / 448) (two roundings of relative size 2^-24 each), so when
+// q' is normal and its 23 fraction bits lie in [48, 2^23 - 4], q has the same exponent k and a fraction above every
+// ties_to_k threshold (at most 44) and below the next power of two: e = k + 1. Returns false (e untouched) otherwise:
+// zero, subnormal or non-finite q', or q' within a few units of a power of two, where mx_exponent_from_amax decides.
+FIM_HD bool mx_exponent_fast(float amax, int& e) {
+  const uint32_t u = f2u(amax * (1.0f / 448.0f));
+  const uint32_t frac = u & 0x7fffffu;
+  if (u < 0x00800000u || u >= 0x7f800000u || frac - 48u > 0x7fffffu - 3u - 48u) return false;
+  e = (int)(u >> 23) - 126;
+  return true;
+}
+
 // round(x / scale) half to even, saturated to +-127 (flashim/quant/formats/int8.py:24-27), IEEE FP32 division.
 FIM_HD int8_t quantize_int8_value(float x, float scale) {
 #ifdef __HIP_DEVICE_COMPILE__

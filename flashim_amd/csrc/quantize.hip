@@ -337,8 +337,8 @@ __global__ __launch_bounds__(256) void quantize_dynamic_kernel(const void* __res
     for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
     amax = fmaxf(amax, __shfl_xor(amax, 1));
     amax = fmaxf(amax, __shfl_xor(amax, 2));
+    const int e = mx_exponent_wave(amax);  // (all lanes: the slow path's branch is wave-uniform)
     if (!live) continue;
-    const int e = mx_exponent_from_amax(amax);
     const float inv = exp2_int(-e);
     uint32_t lo = pack_e4m3x4(mx_scale_clamp(v[0], inv), mx_scale_clamp(v[1], inv), mx_scale_clamp(v[2], inv),
                               mx_scale_clamp(v[3], inv));

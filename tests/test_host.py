@@ -136,6 +136,31 @@ def test_host_mx_exponent_matches_torch_at_every_power_of_two_boundary():
     assert np.array_equal(got, ref.scale_exponent_from_amax(amax).numpy())
 
 
+def test_host_mx_exponent_fast_path_matches_torch():
+    """The division-free exponent (amax * RN(1/448), decided from the product's bits away from powers of two) gives
+    torch's exponent wherever it decides, at every power-of-two boundary and its neighbours and on random amax; it
+    declines zero, subnormal quotients and the few units around each power of two, and decides almost every random
+    value."""
+    h = _host()
+    torch.manual_seed(1)
+    ks = torch.arange(-149, 128).double()
+    steps = torch.cat([torch.arange(0, 64), (1 << 23) - torch.arange(1, 64)]).double()
+    bnd = (torch.exp2(ks)[:, None] * (1 + steps[None] * 2.0**-23) * 448).float().flatten()
+    rnd = torch.rand(1 << 20) * torch.exp2(torch.randint(-140, 120, (1 << 20,)).float())
+    amax = torch.cat([torch.tensor([0.0, 448, 449, 1, 1e-30, 1e-45, 3.4e38]), bnd, bnd.nextafter(torch.tensor(0.0)),
+                      bnd.nextafter(torch.tensor(3e38)), rnd])
+    amax = amax[torch.isfinite(amax)].contiguous()
+    x = amax.numpy()
+    out = np.empty(x.size, np.int8)
+    decided = np.empty(x.size, np.uint8)
+    h.fim_host_mx_exponent_fast(x.ctypes.data_as(ctypes.c_void_p), ctypes.c_int64(x.size),
+                                out.ctypes.data_as(ctypes.c_void_p), decided.ctypes.data_as(ctypes.c_void_p))
+    assert np.array_equal(out, ref.scale_exponent_from_amax(amax).numpy())
+    assert decided[:7].tolist() == [0, 0, 1, 1, 1, 0, 1]  # zero, 448 = 448 x 2^0 and 2^-149 decline
+    tail = decided[-rnd.numel():][rnd.numpy() > 1e-30]  # below 448 x 2^-126 the quotient is subnormal
+    assert tail.mean() > 0.999, tail.mean()
+
+
 def test_host_bf16_and_int8_rounding_match_torch():
     h = _host()
     torch.manual_seed(0)
