@@ -278,6 +278,7 @@ def dwpw_block():
         "mxfp8_one_kernel": lambda: hip_conv.pointwise_mxfp8_fused(*mx),
         "mxfp8_composite": lambda: hip_conv.pointwise_mxfp8_composite(*mx),
         "int8_op": lambda: ops.depthwise5x5_relu_pointwise_int8(*i8),
+        "int8_one_kernel": lambda: hip_conv.pointwise_int8_fused(*i8),
         "int8_composite": lambda: hip_conv.pointwise_int8_composite(*i8),
     }, {"bytes": nbytes}
 

@@ -171,20 +171,6 @@ def _fused_pointwise_shape(value: Tensor, pw_weight: Tensor) -> bool:
     return value.shape[1] == 128 and tuple(pw_weight.shape) == (128, 128)
 
 
-@torch.compiler.assume_constant_result
-def _compute_units(index: int) -> int:
-    return torch.cuda.get_device_properties(index).multi_processor_count
-
-
-def _composite_gemm_is_pointwise_kernel(value: Tensor) -> bool:
-    """Whether the composite's 128-channel GEMM has at least two 256-row tiles per CU, the condition under which the
-    library runs it on its register-operand pointwise kernel: then the two launches are the faster (at 2 x 128 x
-    400 x 400 on MI355X: 89.7 against 94.3 us for the one-kernel block)."""
-    batch, _, height, width = value.shape
-    index = value.device.index if value.device.index is not None else torch.cuda.current_device()
-    return -(-(batch * height * width) // 256) >= 2 * _compute_units(index)
-
-
 def depthwise5x5_relu_pointwise(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
                                 pw_bias: Tensor) -> Tensor:
     """The BF16 refiner block (``flashim/ops/conv.py:67-84``) -> ``[B, C_out, H, W]`` view of NHWC BF16 (channels-last
@@ -200,9 +186,9 @@ def depthwise5x5_relu_pointwise(value: Tensor, dw_weight: Tensor, dw_bias: Tenso
 def depthwise5x5_relu_pointwise_mxfp8(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
                                       pw_scale_swizzled: Tensor, pw_scale_u8: Tensor, pw_bias: Tensor) -> Tensor:
     """The MXFP8 refiner block (``flashim/ops/conv.py:93-113``) -> ``[B, C, H, W]`` view of NHWC BF16. At 128 x 128
-    one kernel (``fim_depthwise5x5_relu_pointwise_mxfp8``: the quantized activations stay on chip) unless the image is
-    large enough for the composite's GEMM to run on the pointwise kernel; otherwise the composite."""
-    if not _fused_pointwise_shape(value, pw_weight) or _composite_gemm_is_pointwise_kernel(value):
+    one kernel (``fim_depthwise5x5_relu_pointwise_mxfp8``: the quantized activations stay on chip), otherwise the
+    two-launch composite."""
+    if not _fused_pointwise_shape(value, pw_weight):
         return pointwise_mxfp8_composite(value, dw_weight, dw_bias, pw_weight, pw_scale_swizzled, pw_scale_u8,
                                          pw_bias)
     return pointwise_mxfp8_fused(value, dw_weight, dw_bias, pw_weight, pw_scale_swizzled, pw_scale_u8, pw_bias)
@@ -237,9 +223,24 @@ def pointwise_mxfp8_composite(value: Tensor, dw_weight: Tensor, dw_bias: Tensor,
 def depthwise5x5_relu_pointwise_int8(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
                                      pw_wscale: Tensor, pw_bias: Tensor, scale: Tensor) -> Tensor:
     """The INT8 refiner block (``flashim/ops/conv.py:119-138``) -> ``[B, C, H, W]`` view of NHWC BF16: the two-launch
-    composite at every shape. Its INT8 intermediate is 1 byte per element, and on MI355X at 2 x 128 x 400 x 400 the
-    composite measured 84 us against 90 us for a one-kernel version, which gave the same bits."""
+    composite at every shape. The one-kernel block (``pointwise_int8_fused``) gives the same bits but measured slower
+    on MI355X at 2 x 128 x 400 x 400 (80 against 68-70 us): the INT8 intermediate is 1 byte per element, so the HBM
+    round trip the fusion saves is small, while the composite's producer runs three workgroups per CU against the
+    one-kernel block's two."""
     return pointwise_int8_composite(value, dw_weight, dw_bias, pw_weight, pw_wscale, pw_bias, scale)
+
+
+def pointwise_int8_fused(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor, pw_wscale: Tensor,
+                         pw_bias: Tensor, scale: Tensor) -> Tensor:
+    """One kernel at C = 128 with a 128 x 128 INT8 pointwise weight; bit for bit the composite."""
+    if not _fused_pointwise_shape(value, pw_weight):
+        raise ValueError(f"the one-kernel block needs C = 128 and a 128 x 128 weight, got {tuple(value.shape)}, "
+                         f"{tuple(pw_weight.shape)}")
+    x, dw_w, dw_b = _dw_operands(value, dw_weight, dw_bias)
+    out = library.depthwise5x5_relu_pointwise_int8(
+        x, dw_w, dw_b, _scalar(scale, value.device), pw_weight.to(value.device).contiguous(),
+        pw_wscale.to(device=value.device, dtype=torch.float32).contiguous(), _bias(pw_bias, value.device))
+    return out.permute(0, 3, 1, 2)
 
 
 def pointwise_int8_composite(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,

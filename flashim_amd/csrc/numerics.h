@@ -113,9 +113,9 @@ FIM_HD int mx_ties_to_k(int k) {
   // -> j < ln2 * 2^(sp_exp - 1 + 23)
   int p = sp_exp - 1 + 23;
   if (p < 0) return 0;
-  // floor(ln2 * 2^p) for p = 0..6 (|k| <= 149 keeps p <= 6)
-  const int table[7] = {0, 1, 2, 5, 11, 22, 44};
-  return table[p > 6 ? 6 : p];
+  // floor(ln2 * 2^p) for p = 0..6 (|k| <= 149 keeps p <= 6): 0, 1, 2, 5, 11, 22, 44; the FP32 product is exact in
+  // its integer part (ln2 is 0.693 and the fraction parts stay 0.07 or more away from the next integer)
+  return (int)(0.69314718f * (float)(1 << (p > 6 ? 6 : p)));
 }
 
 FIM_HD int mx_exponent_from_amax(float amax) {
@@ -186,26 +186,27 @@ FIM_HD int8_t quantize_int8_value(float x, float scale) {
 // when any lane is near a tie), so it neither runs per element nor splits the code that produces the inputs. The
 // saturation is one v_med3_f32 between M - 127 and M + 127 (LO = 0 folds a preceding ReLU in: relu then quantize
 // equals clamping the rounded quotient at 0), so no conversion to an integer is needed: q[i] holds the clamped value's
-// bit pattern, whose low byte is the code (callers keep that byte). 5 VALU operations per value. Checked on the host
+// bit pattern, whose low byte is the code (callers keep that byte). 5 VALU operations per value (FMA, subtraction,
+// residual FMA, running maximum, med3), none on the scalar unit. Checked on the host
 // against round(x / s) on 20M cases including exact ties and their neighbours, with and without the ReLU, and on the
 // GPU byte for byte against the torch references of every INT8 producer.
 template <int N, int LO = -127>
 __device__ __forceinline__ void quantize_int8_fast_n(const float (&x)[N], float scale, float inv, int (&q)[N]) {
   constexpr float M = 12582912.0f;  // 1.5 * 2^23
+  constexpr float NEAR = 0.5f - 0x1p-15f;
   float f[N];
-  bool near[N];
-  bool any = false;
+  // the largest residual of the lane's values, one maximum each (a per-value compare would put each result in a
+  // scalar register pair and OR them on the scalar unit, a dependent chain that cost more than the rest together)
+  float worst = 0.0f;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     f[i] = fmaf(x[i], inv, M);
-    const float r = f[i] - M;
-    near[i] = fabsf(fmaf(x[i], inv, -r)) >= 0.5f - 0x1p-15f;
-    any = any || near[i];
+    worst = fmaxf(worst, fabsf(fmaf(x[i], inv, -(f[i] - M))));
   }
-  if (__builtin_amdgcn_ballot_w64(any) != 0) {
+  if (__builtin_amdgcn_ballot_w64(worst >= NEAR) != 0) {
 #pragma unroll
     for (int i = 0; i < N; ++i)
-      if (near[i]) f[i] = __builtin_rintf(__fdiv_rn(x[i], scale)) + M;
+      if (fabsf(fmaf(x[i], inv, -(f[i] - M))) >= NEAR) f[i] = __builtin_rintf(__fdiv_rn(x[i], scale)) + M;
   }
 #pragma unroll
   for (int i = 0; i < N; ++i) q[i] = __builtin_bit_cast(int, __builtin_amdgcn_fmed3f(f[i], M + (float)LO, M + 127.0f));

@@ -423,6 +423,26 @@ def _(x, dw_weight, dw_bias, pw_weight, pw_e8m0, pw_bias):
     return x.new_empty((b, h, w, pw_weight.shape[0]), dtype=torch.bfloat16)
 
 
+@torch.library.custom_op(f"{NS}::depthwise5x5_relu_pointwise_int8", mutates_args=())
+def depthwise5x5_relu_pointwise_int8(x: Tensor, dw_weight: Tensor, dw_bias: Tensor, scale: Tensor, pw_weight: Tensor,
+                                     pw_wscale: Tensor, pw_bias: Optional[Tensor]) -> Tensor:
+    """The one-kernel INT8 block at C = N = 128: ``x`` BF16 NHWC -> BF16 NHWC ``[B, H, W, N]``; ``scale`` the static
+    activation scale (FP32, one value), ``pw_wscale`` FP32 ``[N]``."""
+    b, h, w, c = x.shape
+    n = pw_weight.shape[0]
+    out = torch.empty(b, h, w, n, device=x.device, dtype=torch.bfloat16)
+    _lib.call("fim_depthwise5x5_relu_pointwise_int8", x.data_ptr(), b, h, w, c, dw_weight.data_ptr(),
+              dw_bias.data_ptr(), scale.data_ptr(), pw_weight.data_ptr(), n, pw_wscale.data_ptr(), _ptr(pw_bias),
+              _bias_code(pw_bias), out.data_ptr(), _stream(x), what=f"depthwise5x5_relu_pointwise_int8 {tuple(x.shape)}")
+    return out
+
+
+@depthwise5x5_relu_pointwise_int8.register_fake
+def _(x, dw_weight, dw_bias, scale, pw_weight, pw_wscale, pw_bias):
+    b, h, w, _ = x.shape
+    return x.new_empty((b, h, w, pw_weight.shape[0]), dtype=torch.bfloat16)
+
+
 # -- the VGG stem ---------------------------------------------------------------------------------------------------
 
 

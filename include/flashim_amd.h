@@ -199,12 +199,21 @@ int fim_depthwise5x5(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t
  * ops.depthwise5x5_relu_pointwise_mxfp8 (flashim/ops/conv.py:93-117); bit for bit the composite (fim_depthwise5x5 then
  * fim_mxfp8_scaled_mm). x BF16 NHWC [B, H, W, 128] (16-byte aligned); dw_weight BF16 [25, 128]; dw_bias FP32 [128];
  * pw_weight [128 (n), 128 (k)] E4M3; pw_scale_e8m0 [128, 4] E8M0 bytes; pw_bias [128] FP32 or BF16 (dtype code as
- * fim_int8_linear) or NULL; out BF16 NHWC [B, H, W, 128]. The INT8 block (flashim/ops/conv.py:119-138) runs as its
- * two-launch composite, fim_depthwise5x5 then fim_int8_linear. */
+ * fim_int8_linear) or NULL; out BF16 NHWC [B, H, W, 128] (16-byte aligned). */
 int fim_depthwise5x5_relu_pointwise_mxfp8(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t C,
                                           const uint16_t* dw_weight, const float* dw_bias, const uint8_t* pw_weight,
                                           int64_t N, const uint8_t* pw_scale_e8m0, const void* pw_bias,
                                           int pw_bias_dtype, uint16_t* out, hipStream_t stream);
+
+/* The INT8 depthwise-then-pointwise refiner block in one kernel at C = N = 128: _dw5x5_relu_int8_pointwise_kernel
+ * (flashim/backends/triton/conv.py:417-475, registered at :585-599) behind ops.depthwise5x5_relu_pointwise_int8
+ * (flashim/ops/conv.py:119-138); bit for bit the composite (fim_depthwise5x5 with the INT8 output, then
+ * fim_int8_linear). act_scale: the static activation scale (one FP32, device); pw_weight INT8 [128 (n), 128 (k)];
+ * pw_wscale FP32 [128]; other operands as fim_depthwise5x5_relu_pointwise_mxfp8. */
+int fim_depthwise5x5_relu_pointwise_int8(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t C,
+                                         const uint16_t* dw_weight, const float* dw_bias, const float* act_scale,
+                                         const int8_t* pw_weight, int64_t N, const float* pw_wscale,
+                                         const void* pw_bias, int pw_bias_dtype, uint16_t* out, hipStream_t stream);
 
 /* The BF16 refiner block's pointwise GEMM: out[m, n] = bf16(sum_k x[m, k] * w[n, k] + bias[n]) with FP32 accumulation.
  * x BF16 [M, K] (16-byte aligned), weight BF16 [N, K] (16-byte aligned), bias FP32 [N] or NULL, out BF16 [M, N]

@@ -247,7 +247,9 @@ def test_pointwise_bf16_rejects_unsupported_shapes():
     assert y.shape == (16, 32) and not y.float().abs().any()
 
 
-FUSED_BLOCK = [(1, (8, 32)), (2, (19, 45)), (1, (3, 5)), (2, (40, 70)), (1, (1, 1))]
+# the last two have more tiles than the persistent grid's workgroups (512 on 256 CUs): each workgroup runs several
+# tiles, prefetching the next tile's first window during the pointwise of the current one
+FUSED_BLOCK = [(1, (8, 32)), (2, (19, 45)), (1, (3, 5)), (2, (40, 70)), (1, (1, 1)), (2, (203, 331)), (1, (400, 400))]
 
 
 @pytest.mark.parametrize("batch,hw", FUSED_BLOCK)
@@ -266,3 +268,25 @@ def test_fused_depthwise_pointwise_matches_composite(batch, hw, bias):
     composite = hip_conv.pointwise_mxfp8_composite(*args)
     assert fused.shape == composite.shape == (batch, channels, *hw)
     assert torch.equal(fused.view(torch.int16), composite.view(torch.int16))
+
+
+@pytest.mark.parametrize("batch,hw", FUSED_BLOCK)
+@pytest.mark.parametrize("bias", ["fp32", "bf16", "none"])
+def test_fused_depthwise_pointwise_int8_matches_composite(batch, hw, bias):
+    """The INT8 block as one kernel (flashim/backends/triton/conv.py:417-475, registered for C = 128 at :585-599):
+    bit for bit the composite (the INT8 depthwise producer, then int8_linear; exact int32 sums, the same FP32
+    epilogue), and the composite within the oracle's bar; a scale small enough that many codes saturate at 127."""
+    channels = 128
+    x, dw_w, dw_b, pw_b, g = _block_inputs(batch, channels, hw, seed=3 * sum(hw) + batch)
+    pw_b = {"fp32": pw_b, "bf16": pw_b.to(torch.bfloat16), "none": None}[bias]
+    dev = lambda ts: [t.to(DEV) if t is not None else None for t in ts]  # noqa: E731
+    pw_w = torch.randint(-127, 128, (channels, channels), dtype=torch.int8, generator=g)
+    pw_s = torch.rand(channels, generator=g) * 0.01 + 0.001
+    for scale in (torch.tensor(0.03), torch.tensor(0.004)):
+        args = dev((x, dw_w, dw_b, pw_w, pw_s, pw_b, scale))
+        fused = hip_conv.pointwise_int8_fused(*args)
+        composite = hip_conv.pointwise_int8_composite(*args)
+        assert fused.shape == composite.shape == (batch, channels, *hw)
+        assert torch.equal(fused.view(torch.int16), composite.view(torch.int16))
+        assert torch.equal(ops.depthwise5x5_relu_pointwise_int8.get("hip")(*args).view(torch.int16),
+                           composite.view(torch.int16))
