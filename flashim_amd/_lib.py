@@ -57,12 +57,12 @@ SIGNATURES: dict[str, list] = {
                         _vp],
     "fim_conv3x3_small_cin_quantize_int8": [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _vp],
     "fim_bias_relu_quantize_int8": [_vp, _i64, _i64, _i64, _i64, _vp, _i32, _vp, _vp, _vp],
-    "fim_depthwise5x5": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp],
-    "fim_pointwise_bf16": [_vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp],
-    "fim_depthwise5x5_relu_pointwise_mxfp8": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _vp,
-                                              _vp],
-    "fim_depthwise5x5_relu_pointwise_int8": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i32,
-                                             _vp, _vp],
+    "fim_depthwise5x5": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp],
+    "fim_pointwise_bf16": [_vp, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _vp],
+    "fim_depthwise5x5_relu_pointwise_mxfp8": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _vp, _vp, _i32,
+                                              _vp, _vp],
+    "fim_depthwise5x5_relu_pointwise_int8": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i64, _vp, _vp,
+                                             _i32, _vp, _vp],
 }
 
 # the probe library (csrc/probe.h): test and measurement hooks, not part of the product ABI

@@ -126,8 +126,9 @@ def _nhwc_bf16(value: Tensor) -> Tensor:
 
 
 def _dw_operands(value: Tensor, weight: Tensor, bias: Tensor) -> tuple[Tensor, Tensor, Tensor]:
-    return (_nhwc_bf16(value), weight.to(device=value.device, dtype=torch.bfloat16).contiguous(),
-            bias.to(device=value.device, dtype=torch.float32).contiguous())
+    """BF16 NHWC input, BF16 weight, and the bias as given when it is FP32 or BF16 (the kernels read either; the
+    BF16 -> FP32 widening is exact), else widened to FP32."""
+    return (_nhwc_bf16(value), weight.to(device=value.device, dtype=torch.bfloat16).contiguous(), _bias(bias, value.device))
 
 
 def depthwise5x5_relu_mxfp8(value: Tensor, weight: Tensor, bias: Tensor) -> tuple[Tensor, Tensor]:
@@ -179,7 +180,7 @@ def depthwise5x5_relu_pointwise(value: Tensor, dw_weight: Tensor, dw_bias: Tenso
     batch, _, height, width = value.shape
     hidden = library.depthwise5x5(*_dw_operands(value, dw_weight, dw_bias), 0, library.DW_BF16, None, None)
     out = library.pointwise_bf16(hidden, pw_weight.to(device=value.device, dtype=torch.bfloat16).contiguous(),
-                                 pw_bias.to(device=value.device, dtype=torch.float32).contiguous())
+                                 _bias(pw_bias, value.device))
     return out.reshape(batch, height, width, -1).permute(0, 3, 1, 2)
 
 

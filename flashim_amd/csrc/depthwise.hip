@@ -24,7 +24,8 @@ enum { DW_MX_DYNAMIC = 0, DW_INT8 = 1, DW_BF16 = 2, DW_MX_STATIC = 3 };
 struct DwArgs {
   const uint16_t* x;
   const uint16_t* w;
-  const float* bias;
+  const void* bias;        // FP32 or BF16 [C]
+  int bias_bf16;
   const float* scale;      // INT8
   const int8_t* expo;      // MX static [C / 32]
   void* out;
@@ -126,7 +127,8 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
     wa[ky][0] = __builtin_bit_cast(v4bf16, v << (16 * r4));
     wa[ky][1] = __builtin_bit_cast(v4bf16, u >> (16 * (3 - r4)));
   }
-  const float bias = a.bias[ch];
+  const float bias = a.bias_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(a.bias)[ch])
+                                 : static_cast<const float*>(a.bias)[ch];
   const v4f biasv = {bias, bias, bias, bias};
 
   // stage the (DW_TH + 4) x (DW_TW + 4) x 32 halo tile: every load of the thread's units is issued before the first
@@ -386,9 +388,10 @@ extern "C" {
 // act: 0 ReLU, 1 GELU. out_mode: 0 MXFP8 dynamic (e4m3 out + exponents / swizzled scales), 1 INT8 (scale),
 // 2 BF16, 3 MXFP8 static (exponent [C/32]).
 int fim_depthwise5x5(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t C, const uint16_t* weight,
-                     const float* bias, int act, int out_mode, const float* scale, const int8_t* exponent, void* out,
-                     int8_t* exponent_out, uint8_t* swizzled, hipStream_t stream) {
+                     const void* bias, int bias_dtype, int act, int out_mode, const float* scale,
+                     const int8_t* exponent, void* out, int8_t* exponent_out, uint8_t* swizzled, hipStream_t stream) {
   if (x == nullptr || weight == nullptr || bias == nullptr || out == nullptr) return FIM_ERR_INVALID;
+  if (bias_dtype != FIM_F32 && bias_dtype != FIM_BF16) return FIM_ERR_INVALID;
   if (B < 0 || H < 0 || W < 0 || C <= 0) return FIM_ERR_INVALID;
   if (out_mode < 0 || out_mode > 3 || act < 0 || act > 1) return FIM_ERR_INVALID;
   if (out_mode == DW_INT8 && scale == nullptr) return FIM_ERR_INVALID;
@@ -405,7 +408,7 @@ int fim_depthwise5x5(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t
   const int64_t tx = cdiv(W, DW_TW), ty = cdiv(H, DW_TH);
   const int64_t ntiles = tx * ty * B * (C / DW_CS);
   if (ntiles > (1LL << 31) - 8) return FIM_ERR_UNSUPPORTED;
-  DwArgs a{x, weight, bias, scale, exponent, out, swizzled, exponent_out, (int)B, (int)H, (int)W, (int)C,
+  DwArgs a{x, weight, bias, bias_dtype == FIM_BF16, scale, exponent, out, swizzled, exponent_out, (int)B, (int)H, (int)W, (int)C,
            (int)tx, (int)ty, ntiles};
   dim3 grid((unsigned)(cdiv(ntiles, 8) * 8));  // a multiple of the 8 XCDs: the kernel maps pids to tiles per XCD
   if (act == ACT_RELU)

@@ -37,7 +37,8 @@ static_assert(4 * DP_OROW <= DP_STAGE, "a 4-row output half fits in the input wi
 struct DwPwArgs {
   const uint16_t* x;        // BF16 [B, H, W, 128]
   const uint16_t* dw_w;     // BF16 [25, 128]
-  const float* dw_b;        // FP32 [128]
+  const void* dw_b;         // FP32 or BF16 [128]
+  int dw_b_bf16;
   const uint8_t* pw_w;      // E4M3 or INT8 [128, 128]
   const uint8_t* pw_e8m0;   // MXFP8: [128, 4] E8M0 bytes
   const float* act_scale;   // INT8: the static activation scale (one value)
@@ -117,7 +118,7 @@ __global__ __launch_bounds__(256, 2) void dw_pw_kernel(const DwPwArgs a) {
     const int ch = s * DP_CS + 16 * cg + bch;
 #pragma unroll
     for (int k = 0; k < 25; ++k) wpre[k] = a.dw_w[k * DP_C + ch];
-    bpre = a.dw_b[ch];
+    bpre = a.dw_b_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(a.dw_b)[ch]) : static_cast<const float*>(a.dw_b)[ch];
   };
   int cx0, cy0, cb;
   origin(tile, cx0, cy0, cb);
@@ -406,23 +407,26 @@ static bool dwpw_dims_ok(int64_t B, int64_t H, int64_t W, int64_t C) {
 extern "C" {
 
 int fim_depthwise5x5_relu_pointwise_mxfp8(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t C,
-                                          const uint16_t* dw_weight, const float* dw_bias, const uint8_t* pw_weight,
-                                          int64_t N, const uint8_t* pw_scale_e8m0, const void* pw_bias,
-                                          int pw_bias_dtype, uint16_t* out, hipStream_t stream) {
+                                          const uint16_t* dw_weight, const void* dw_bias, int dw_bias_dtype,
+                                          const uint8_t* pw_weight, int64_t N, const uint8_t* pw_scale_e8m0,
+                                          const void* pw_bias, int pw_bias_dtype, uint16_t* out, hipStream_t stream) {
   if (pw_scale_e8m0 == nullptr || ((uintptr_t)pw_scale_e8m0 % 4) != 0) return FIM_ERR_INVALID;
+  if (dw_bias_dtype != FIM_F32 && dw_bias_dtype != FIM_BF16) return FIM_ERR_INVALID;
   if (!dwpw_dims_ok(B, H, W, C)) return FIM_ERR_UNSUPPORTED;
-  DwPwArgs a{x, dw_weight, dw_bias, pw_weight, pw_scale_e8m0, nullptr, nullptr, pw_bias, pw_bias_dtype, out,
+  DwPwArgs a{x, dw_weight, dw_bias, dw_bias_dtype == FIM_BF16, pw_weight, pw_scale_e8m0, nullptr, nullptr, pw_bias, pw_bias_dtype, out,
              (int)B, (int)H, (int)W, 0, 0, 0};
   return dwpw_launch(a, DP_MX, C, N, stream);
 }
 
 int fim_depthwise5x5_relu_pointwise_int8(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t C,
-                                         const uint16_t* dw_weight, const float* dw_bias, const float* act_scale,
-                                         const int8_t* pw_weight, int64_t N, const float* pw_wscale,
-                                         const void* pw_bias, int pw_bias_dtype, uint16_t* out, hipStream_t stream) {
+                                         const uint16_t* dw_weight, const void* dw_bias, int dw_bias_dtype,
+                                         const float* act_scale, const int8_t* pw_weight, int64_t N,
+                                         const float* pw_wscale, const void* pw_bias, int pw_bias_dtype, uint16_t* out,
+                                         hipStream_t stream) {
   if (act_scale == nullptr || pw_wscale == nullptr) return FIM_ERR_INVALID;
+  if (dw_bias_dtype != FIM_F32 && dw_bias_dtype != FIM_BF16) return FIM_ERR_INVALID;
   if (!dwpw_dims_ok(B, H, W, C)) return FIM_ERR_UNSUPPORTED;
-  DwPwArgs a{x, dw_weight, dw_bias, reinterpret_cast<const uint8_t*>(pw_weight), nullptr, act_scale, pw_wscale,
+  DwPwArgs a{x, dw_weight, dw_bias, dw_bias_dtype == FIM_BF16, reinterpret_cast<const uint8_t*>(pw_weight), nullptr, act_scale, pw_wscale,
              pw_bias, pw_bias_dtype, out, (int)B, (int)H, (int)W, 0, 0, 0};
   return dwpw_launch(a, DP_INT8, C, N, stream);
 }

@@ -26,8 +26,8 @@ constexpr int PW_WAVES = 4;
 
 template <int KS, int NB>
 __global__ __launch_bounds__(256) void pw_bf16_kernel(const uint16_t* __restrict__ x, int64_t M,
-                                                      const uint16_t* __restrict__ w, const float* __restrict__ bias,
-                                                      uint16_t* __restrict__ out, int64_t nblocks) {
+                                                      const uint16_t* __restrict__ w, const void* __restrict__ bias,
+                                                      int bias_bf16, uint16_t* __restrict__ out, int64_t nblocks) {
   constexpr int K = 32 * KS, N = 16 * NB;
   constexpr int WROW = K + 8;  // BF16 elements per staged weight row
   __shared__ __align__(16) uint16_t sw[N * WROW];
@@ -40,7 +40,10 @@ __global__ __launch_bounds__(256) void pw_bf16_kernel(const uint16_t* __restrict
     const int r = i / (K / 8), c = i % (K / 8);
     *reinterpret_cast<uint4*>(&sw[r * WROW + 8 * c]) = *reinterpret_cast<const uint4*>(&w[(int64_t)r * K + 8 * c]);
   }
-  for (int i = threadIdx.x; i < N; i += 256) sb[i] = bias != nullptr ? bias[i] : -0.0f;
+  for (int i = threadIdx.x; i < N; i += 256)
+    sb[i] = bias == nullptr ? -0.0f
+            : bias_bf16     ? bf16_to_f32(static_cast<const uint16_t*>(bias)[i])
+                            : static_cast<const float*>(bias)[i];
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
@@ -104,16 +107,16 @@ __global__ __launch_bounds__(256) void pw_bf16_kernel(const uint16_t* __restrict
 
 template <int KS>
 static void pw_launch_n(int nb, dim3 grid, hipStream_t s, const uint16_t* x, int64_t M, const uint16_t* w,
-                        const float* bias, uint16_t* out, int64_t nblocks) {
+                        const void* bias, int bias_bf16, uint16_t* out, int64_t nblocks) {
   switch (nb) {
-    case 1: pw_bf16_kernel<KS, 1><<<grid, dim3(256), 0, s>>>(x, M, w, bias, out, nblocks); break;
-    case 2: pw_bf16_kernel<KS, 2><<<grid, dim3(256), 0, s>>>(x, M, w, bias, out, nblocks); break;
-    case 3: pw_bf16_kernel<KS, 3><<<grid, dim3(256), 0, s>>>(x, M, w, bias, out, nblocks); break;
-    case 4: pw_bf16_kernel<KS, 4><<<grid, dim3(256), 0, s>>>(x, M, w, bias, out, nblocks); break;
-    case 5: pw_bf16_kernel<KS, 5><<<grid, dim3(256), 0, s>>>(x, M, w, bias, out, nblocks); break;
-    case 6: pw_bf16_kernel<KS, 6><<<grid, dim3(256), 0, s>>>(x, M, w, bias, out, nblocks); break;
-    case 7: pw_bf16_kernel<KS, 7><<<grid, dim3(256), 0, s>>>(x, M, w, bias, out, nblocks); break;
-    default: pw_bf16_kernel<KS, 8><<<grid, dim3(256), 0, s>>>(x, M, w, bias, out, nblocks); break;
+    case 1: pw_bf16_kernel<KS, 1><<<grid, dim3(256), 0, s>>>(x, M, w, bias, bias_bf16, out, nblocks); break;
+    case 2: pw_bf16_kernel<KS, 2><<<grid, dim3(256), 0, s>>>(x, M, w, bias, bias_bf16, out, nblocks); break;
+    case 3: pw_bf16_kernel<KS, 3><<<grid, dim3(256), 0, s>>>(x, M, w, bias, bias_bf16, out, nblocks); break;
+    case 4: pw_bf16_kernel<KS, 4><<<grid, dim3(256), 0, s>>>(x, M, w, bias, bias_bf16, out, nblocks); break;
+    case 5: pw_bf16_kernel<KS, 5><<<grid, dim3(256), 0, s>>>(x, M, w, bias, bias_bf16, out, nblocks); break;
+    case 6: pw_bf16_kernel<KS, 6><<<grid, dim3(256), 0, s>>>(x, M, w, bias, bias_bf16, out, nblocks); break;
+    case 7: pw_bf16_kernel<KS, 7><<<grid, dim3(256), 0, s>>>(x, M, w, bias, bias_bf16, out, nblocks); break;
+    default: pw_bf16_kernel<KS, 8><<<grid, dim3(256), 0, s>>>(x, M, w, bias, bias_bf16, out, nblocks); break;
   }
 }
 
@@ -123,9 +126,11 @@ using namespace fim;
 
 extern "C" {
 
-int fim_pointwise_bf16(const uint16_t* x, int64_t M, int64_t K, const uint16_t* weight, int64_t N, const float* bias,
-                       uint16_t* out, hipStream_t stream) {
+int fim_pointwise_bf16(const uint16_t* x, int64_t M, int64_t K, const uint16_t* weight, int64_t N, const void* bias,
+                       int bias_dtype, uint16_t* out, hipStream_t stream) {
   if (x == nullptr || weight == nullptr || out == nullptr || M < 0 || K <= 0 || N <= 0) return FIM_ERR_INVALID;
+  if (bias_dtype != FIM_F32 && bias_dtype != FIM_BF16) return FIM_ERR_INVALID;
+  const int bias_bf16 = bias_dtype == FIM_BF16;
   if (K % 32 != 0 || K > 128 || N % 16 != 0 || N > 128) return FIM_ERR_UNSUPPORTED;
   if (((uintptr_t)x % 16) != 0 || ((uintptr_t)weight % 16) != 0 || ((uintptr_t)out % 16) != 0) return FIM_ERR_UNSUPPORTED;
   if (M == 0) return FIM_OK;
@@ -134,10 +139,10 @@ int fim_pointwise_bf16(const uint16_t* x, int64_t M, int64_t K, const uint16_t* 
   const int64_t wgs = std::min<int64_t>(cdiv(nblocks, PW_WAVES), 2048);
   const dim3 grid((unsigned)wgs);
   switch (K / 32) {
-    case 1: pw_launch_n<1>((int)(N / 16), grid, stream, x, M, weight, bias, out, nblocks); break;
-    case 2: pw_launch_n<2>((int)(N / 16), grid, stream, x, M, weight, bias, out, nblocks); break;
-    case 3: pw_launch_n<3>((int)(N / 16), grid, stream, x, M, weight, bias, out, nblocks); break;
-    default: pw_launch_n<4>((int)(N / 16), grid, stream, x, M, weight, bias, out, nblocks); break;
+    case 1: pw_launch_n<1>((int)(N / 16), grid, stream, x, M, weight, bias, bias_bf16, out, nblocks); break;
+    case 2: pw_launch_n<2>((int)(N / 16), grid, stream, x, M, weight, bias, bias_bf16, out, nblocks); break;
+    case 3: pw_launch_n<3>((int)(N / 16), grid, stream, x, M, weight, bias, bias_bf16, out, nblocks); break;
+    default: pw_launch_n<4>((int)(N / 16), grid, stream, x, M, weight, bias, bias_bf16, out, nblocks); break;
   }
   return launch_status();
 }

@@ -371,8 +371,8 @@ def depthwise5x5(x: Tensor, weight: Tensor, bias: Tensor, act: int, mode: int, s
     """``x`` BF16 NHWC ``[B, H, W, C]`` -> ``[B*H*W, C]``: INT8 (mode 1), BF16 (2) or E4M3 codes (3, ``uint8``)."""
     b, h, w, c = x.shape
     out = torch.empty(b * h * w, c, device=x.device, dtype=_DW_OUT_DTYPE[mode])
-    _lib.call("fim_depthwise5x5", x.data_ptr(), b, h, w, c, weight.data_ptr(), bias.data_ptr(), act, mode,
-              _ptr(scale), _ptr(exponent), out.data_ptr(), None, None, _stream(x),
+    _lib.call("fim_depthwise5x5", x.data_ptr(), b, h, w, c, weight.data_ptr(), bias.data_ptr(), _bias_code(bias), act,
+              mode, _ptr(scale), _ptr(exponent), out.data_ptr(), None, None, _stream(x),
               what=f"depthwise5x5 {tuple(x.shape)}")
     return out
 
@@ -391,8 +391,9 @@ def depthwise5x5_mx_dynamic(x: Tensor, weight: Tensor, bias: Tensor) -> tuple[Te
     out = torch.empty(rows, c, device=x.device, dtype=torch.uint8)
     size = -(-rows // 128) * 128 * -(-groups // 4) * 4
     swz = (torch.zeros if rows % 128 or groups % 4 else torch.empty)(size, device=x.device, dtype=torch.uint8)
-    _lib.call("fim_depthwise5x5", x.data_ptr(), b, h, w, c, weight.data_ptr(), bias.data_ptr(), 0, DW_MX_DYNAMIC,
-              None, None, out.data_ptr(), None, swz.data_ptr(), _stream(x), what=f"depthwise5x5 {tuple(x.shape)}")
+    _lib.call("fim_depthwise5x5", x.data_ptr(), b, h, w, c, weight.data_ptr(), bias.data_ptr(), _bias_code(bias), 0,
+              DW_MX_DYNAMIC, None, None, out.data_ptr(), None, swz.data_ptr(), _stream(x),
+              what=f"depthwise5x5 {tuple(x.shape)}")
     return out, swz
 
 
@@ -412,7 +413,8 @@ def depthwise5x5_relu_pointwise_mxfp8(x: Tensor, dw_weight: Tensor, dw_bias: Ten
     n = pw_weight.shape[0]
     out = torch.empty(b, h, w, n, device=x.device, dtype=torch.bfloat16)
     _lib.call("fim_depthwise5x5_relu_pointwise_mxfp8", x.data_ptr(), b, h, w, c, dw_weight.data_ptr(),
-              dw_bias.data_ptr(), pw_weight.data_ptr(), n, pw_e8m0.data_ptr(), _ptr(pw_bias), _bias_code(pw_bias),
+              dw_bias.data_ptr(), _bias_code(dw_bias), pw_weight.data_ptr(), n, pw_e8m0.data_ptr(), _ptr(pw_bias),
+              _bias_code(pw_bias),
               out.data_ptr(), _stream(x), what=f"depthwise5x5_relu_pointwise_mxfp8 {tuple(x.shape)}")
     return out
 
@@ -432,7 +434,8 @@ def depthwise5x5_relu_pointwise_int8(x: Tensor, dw_weight: Tensor, dw_bias: Tens
     n = pw_weight.shape[0]
     out = torch.empty(b, h, w, n, device=x.device, dtype=torch.bfloat16)
     _lib.call("fim_depthwise5x5_relu_pointwise_int8", x.data_ptr(), b, h, w, c, dw_weight.data_ptr(),
-              dw_bias.data_ptr(), scale.data_ptr(), pw_weight.data_ptr(), n, pw_wscale.data_ptr(), _ptr(pw_bias),
+              dw_bias.data_ptr(), _bias_code(dw_bias), scale.data_ptr(), pw_weight.data_ptr(), n, pw_wscale.data_ptr(),
+              _ptr(pw_bias),
               _bias_code(pw_bias), out.data_ptr(), _stream(x), what=f"depthwise5x5_relu_pointwise_int8 {tuple(x.shape)}")
     return out
 
@@ -480,11 +483,12 @@ def _(raw, bias, scale):
 
 @torch.library.custom_op(f"{NS}::pointwise_bf16", mutates_args=())
 def pointwise_bf16(x: Tensor, weight: Tensor, bias: Optional[Tensor]) -> Tensor:
-    """``x`` BF16 ``[M, K]`` times ``weight`` BF16 ``[N, K]`` transposed, plus FP32 ``bias`` -> BF16 ``[M, N]``."""
+    """``x`` BF16 ``[M, K]`` times ``weight`` BF16 ``[N, K]`` transposed, plus FP32 or BF16 ``bias`` -> BF16 ``[M, N]``."""
     m, k = x.shape
     n = weight.shape[0]
     out = torch.empty(m, n, device=x.device, dtype=torch.bfloat16)
-    _lib.call("fim_pointwise_bf16", x.data_ptr(), m, k, weight.data_ptr(), n, _ptr(bias), out.data_ptr(), _stream(x),
+    _lib.call("fim_pointwise_bf16", x.data_ptr(), m, k, weight.data_ptr(), n, _ptr(bias), _bias_code(bias),
+              out.data_ptr(), _stream(x),
               what=f"pointwise_bf16 {m}x{k}x{n}")
     return out
 

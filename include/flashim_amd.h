@@ -183,27 +183,28 @@ int fim_im2col_gather(const uint8_t* x, int64_t B, int64_t H, int64_t W, int64_t
 /* ---- depthwise 5x5 producers -------------------------------------------------------------------------------- */
 
 /* Depthwise 5x5, pad 2: x BF16 NHWC [B, H, W, C] (channels-last [B, C, H, W]), weight BF16 [25, C] (ky, kx major),
- * bias FP32 [C], C % 32 == 0. act 0: relu(conv + bias) in FP32; act 1: gelu(bf16(conv + bias)) rounded to BF16.
+ * bias [C] FP32 (bias_dtype 0) or BF16 (1), C % 32 == 0. act 0: relu(conv + bias) in FP32; act 1: gelu(bf16(conv + bias)) rounded to BF16.
  * out_mode 0: dynamic per-(pixel, 32) MXFP8, E4M3 out [B*H*W, C] + exponent_out [B*H*W, C/32] and/or the swizzled
  * E8M0 bytes (either may be NULL); 1: static INT8 of the BF16-rounded value with *scale; 2: BF16 out;
  * 3: static MXFP8 with exponent [C/32]. act 0 + mode 0 replaces ops.depthwise5x5_relu_mxfp8 (flashim/ops/conv.py:30-44),
  * act 0 + mode 1 replaces ops.depthwise5x5_relu_int8 (flashim/ops/conv.py:50-61; the CUDA launcher it mirrors is
  * launch_dw5x5_relu_int8, flashim/backends/cuda/csrc/depthwise.cu:407-412). */
 int fim_depthwise5x5(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t C, const uint16_t* weight,
-                     const float* bias, int act, int out_mode, const float* scale, const int8_t* exponent, void* out,
-                     int8_t* exponent_out, uint8_t* swizzled, hipStream_t stream);
+                     const void* bias, int bias_dtype, int act, int out_mode, const float* scale,
+                     const int8_t* exponent, void* out, int8_t* exponent_out, uint8_t* swizzled, hipStream_t stream);
 
 /* The MXFP8 depthwise-then-pointwise refiner block in one kernel, for C = 128 and a 128 x 128 pointwise weight (the
  * reference's fused shape; other shapes return 99 and take the two-launch composite). Replaces the fused Triton kernel
  * _dw5x5_relu_mx_pointwise_kernel (flashim/backends/triton/conv.py:310-420) behind
  * ops.depthwise5x5_relu_pointwise_mxfp8 (flashim/ops/conv.py:93-117); bit for bit the composite (fim_depthwise5x5 then
- * fim_mxfp8_scaled_mm). x BF16 NHWC [B, H, W, 128] (16-byte aligned); dw_weight BF16 [25, 128]; dw_bias FP32 [128];
+ * fim_mxfp8_scaled_mm). x BF16 NHWC [B, H, W, 128] (16-byte aligned); dw_weight BF16 [25, 128]; dw_bias [128] FP32
+ * (dw_bias_dtype 0) or BF16 (1);
  * pw_weight [128 (n), 128 (k)] E4M3; pw_scale_e8m0 [128, 4] E8M0 bytes; pw_bias [128] FP32 or BF16 (dtype code as
  * fim_int8_linear) or NULL; out BF16 NHWC [B, H, W, 128] (16-byte aligned). */
 int fim_depthwise5x5_relu_pointwise_mxfp8(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t C,
-                                          const uint16_t* dw_weight, const float* dw_bias, const uint8_t* pw_weight,
-                                          int64_t N, const uint8_t* pw_scale_e8m0, const void* pw_bias,
-                                          int pw_bias_dtype, uint16_t* out, hipStream_t stream);
+                                          const uint16_t* dw_weight, const void* dw_bias, int dw_bias_dtype,
+                                          const uint8_t* pw_weight, int64_t N, const uint8_t* pw_scale_e8m0,
+                                          const void* pw_bias, int pw_bias_dtype, uint16_t* out, hipStream_t stream);
 
 /* The INT8 depthwise-then-pointwise refiner block in one kernel at C = N = 128: _dw5x5_relu_int8_pointwise_kernel
  * (flashim/backends/triton/conv.py:417-475, registered at :585-599) behind ops.depthwise5x5_relu_pointwise_int8
@@ -211,17 +212,19 @@ int fim_depthwise5x5_relu_pointwise_mxfp8(const uint16_t* x, int64_t B, int64_t 
  * fim_int8_linear). act_scale: the static activation scale (one FP32, device); pw_weight INT8 [128 (n), 128 (k)];
  * pw_wscale FP32 [128]; other operands as fim_depthwise5x5_relu_pointwise_mxfp8. */
 int fim_depthwise5x5_relu_pointwise_int8(const uint16_t* x, int64_t B, int64_t H, int64_t W, int64_t C,
-                                         const uint16_t* dw_weight, const float* dw_bias, const float* act_scale,
-                                         const int8_t* pw_weight, int64_t N, const float* pw_wscale,
-                                         const void* pw_bias, int pw_bias_dtype, uint16_t* out, hipStream_t stream);
+                                         const uint16_t* dw_weight, const void* dw_bias, int dw_bias_dtype,
+                                         const float* act_scale, const int8_t* pw_weight, int64_t N,
+                                         const float* pw_wscale, const void* pw_bias, int pw_bias_dtype, uint16_t* out,
+                                         hipStream_t stream);
 
 /* The BF16 refiner block's pointwise GEMM: out[m, n] = bf16(sum_k x[m, k] * w[n, k] + bias[n]) with FP32 accumulation.
- * x BF16 [M, K] (16-byte aligned), weight BF16 [N, K] (16-byte aligned), bias FP32 [N] or NULL, out BF16 [M, N]
+ * x BF16 [M, K] (16-byte aligned), weight BF16 [N, K] (16-byte aligned), bias [N] FP32 (bias_dtype 0) or BF16 (1) or
+ * NULL, out BF16 [M, N]
  * (16-byte aligned); K in {32, 64, 96, 128}, N a multiple of 16 up to 128 (else 99). With fim_depthwise5x5 (act 0, out_mode 2) it
  * replaces the fused BF16 block behind ops.depthwise5x5_relu_pointwise (flashim/ops/conv.py:67-84; the CUDA launcher
  * it stands for is launch_depthwise5x5_relu_pointwise, flashim/backends/cuda/conv.py:194-209). */
-int fim_pointwise_bf16(const uint16_t* x, int64_t M, int64_t K, const uint16_t* weight, int64_t N, const float* bias,
-                       uint16_t* out, hipStream_t stream);
+int fim_pointwise_bf16(const uint16_t* x, int64_t M, int64_t K, const uint16_t* weight, int64_t N, const void* bias,
+                       int bias_dtype, uint16_t* out, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -72,10 +72,12 @@ def test_depthwise_rejects_channel_counts_past_its_32_bit_indexing():
     lib = _lib.load()
     fake = 1 << 20  # 16-byte aligned stand-ins: the call must return before touching memory or launching
     c = 85899360  # a multiple of 32 above INT32_MAX / 25 (the weight index (ky * 5 + kx) * C + c)
-    assert lib.fim_depthwise5x5(fake, 1, 1, 1, c, fake, fake, 0, 2, None, None, fake, None, None,
+    assert lib.fim_depthwise5x5(fake, 1, 1, 1, c, fake, fake, 0, 0, 2, None, None, fake, None, None,
                                 None) == _lib.FIM_ERR_UNSUPPORTED
-    assert lib.fim_depthwise5x5(fake, 1 << 20, 1 << 10, 1 << 10, 32, fake, fake, 0, 2, None, None, fake, None, None,
+    assert lib.fim_depthwise5x5(fake, 1 << 20, 1 << 10, 1 << 10, 32, fake, fake, 0, 0, 2, None, None, fake, None, None,
                                 None) == _lib.FIM_ERR_UNSUPPORTED  # 2^45 elements
+    assert lib.fim_depthwise5x5(fake, 1, 1, 1, 32, fake, fake, 2, 0, 2, None, None, fake, None, None,
+                                None) == _lib.FIM_ERR_INVALID  # bias dtype code
 
 
 def test_int8_linear_quantize_rejects_a_row_stride_below_n():
