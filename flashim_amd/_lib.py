@@ -51,7 +51,7 @@ SIGNATURES: dict[str, list] = {
         _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _i64, _i64, _vp, _vp, _vp,
     ],
     "fim_int8_linear_quantize": [_vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _vp],
-    "fim_mxfp8_scaled_mm": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i32, _vp, _vp],
+    "fim_mxfp8_scaled_mm": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _i32, _vp, _i32, _vp, _vp],
     "fim_im2col_gather": [_vp, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp],
     "fim_refiner_mlp": [_i32, _i32, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _vp,
                         _vp],

@@ -172,6 +172,27 @@ def _fused_pointwise_shape(value: Tensor, pw_weight: Tensor) -> bool:
     return value.shape[1] == 128 and tuple(pw_weight.shape) == (128, 128)
 
 
+@torch.compiler.assume_constant_result
+def _compute_units(index: int) -> int:
+    return torch.cuda.get_device_properties(index).multi_processor_count
+
+
+def _one_kernel_block_wins(value: Tensor) -> bool:
+    """Whether the one-kernel depthwise-pointwise block beats its two-launch composite at this image: it takes
+    32 x 8-pixel tiles with all 128 channels on a workgroup (two per CU), so with few tiles each workgroup's four
+    channel slices in sequence are the latency, and with many the composite's producer (three workgroups per CU, one
+    channel slice each) and pointwise GEMM run faster. Measured on MI355X (256 CUs), MXFP8 / INT8, us, one kernel
+    against composite: 140 tiles 20.7 / 18.0 and 23.2 / 18.9; 200 tiles 22.0 / 23.9 and 24.4 / 26.0; 256 tiles
+    23.5 / 24.7 and 26.3 / 27.6; 456 tiles 29.3 / 42.2 and 31.5 / 40.1; 520 tiles 43.3 / 43.4 and 47.0 / 42.4; 675 tiles
+    44.1 / 42.4 and 49.0 / 44.5; 1300 tiles (2 x 400 x 400) 74.5 / 65.0 and 81.0 / 69.0. Hence the band
+    [3/4, 2] x CUs."""
+    batch, _, height, width = value.shape
+    tiles = batch * -(-height // 8) * -(-width // 32)
+    index = value.device.index if value.device.index is not None else torch.cuda.current_device()
+    cus = _compute_units(index)
+    return 3 * cus <= 4 * tiles <= 8 * cus
+
+
 def depthwise5x5_relu_pointwise(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
                                 pw_bias: Tensor) -> Tensor:
     """The BF16 refiner block (``flashim/ops/conv.py:67-84``) -> ``[B, C_out, H, W]`` view of NHWC BF16 (channels-last
@@ -186,10 +207,10 @@ def depthwise5x5_relu_pointwise(value: Tensor, dw_weight: Tensor, dw_bias: Tenso
 
 def depthwise5x5_relu_pointwise_mxfp8(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
                                       pw_scale_swizzled: Tensor, pw_scale_u8: Tensor, pw_bias: Tensor) -> Tensor:
-    """The MXFP8 refiner block (``flashim/ops/conv.py:93-113``) -> ``[B, C, H, W]`` view of NHWC BF16. At 128 x 128
-    one kernel (``fim_depthwise5x5_relu_pointwise_mxfp8``: the quantized activations stay on chip), otherwise the
-    two-launch composite."""
-    if not _fused_pointwise_shape(value, pw_weight):
+    """The MXFP8 refiner block (``flashim/ops/conv.py:93-113``) -> ``[B, C, H, W]`` view of NHWC BF16: one kernel
+    (``fim_depthwise5x5_relu_pointwise_mxfp8``: the quantized activations stay on chip) at 128 x 128 where it is the
+    faster (``_one_kernel_block_wins``), otherwise the two-launch composite."""
+    if not (_fused_pointwise_shape(value, pw_weight) and _one_kernel_block_wins(value)):
         return pointwise_mxfp8_composite(value, dw_weight, dw_bias, pw_weight, pw_scale_swizzled, pw_scale_u8,
                                          pw_bias)
     return pointwise_mxfp8_fused(value, dw_weight, dw_bias, pw_weight, pw_scale_swizzled, pw_scale_u8, pw_bias)
@@ -215,19 +236,20 @@ def pointwise_mxfp8_composite(value: Tensor, dw_weight: Tensor, dw_bias: Tensor,
     batch, _, height, width = value.shape
     codes, swizzled = library.depthwise5x5_mx_dynamic(*_dw_operands(value, dw_weight, dw_bias))
     n, k = pw_weight.shape
-    w_exponent = (pw_scale_u8.view(torch.uint8).to(torch.int16) - 127).to(torch.int8).reshape(n, k // 32)
-    out = library.mxfp8_scaled_mm(codes, swizzled, pw_weight.contiguous().view(torch.uint8),
-                                  w_exponent.to(value.device).contiguous(), _bias(pw_bias, value.device))
+    # the weight's E8M0 bytes go to the GEMM as they are (no per-call conversion to signed exponents)
+    w_e8m0 = pw_scale_u8.to(value.device).contiguous().view(torch.int8).reshape(n, k // 32)
+    out = library.mxfp8_scaled_mm(codes, swizzled, pw_weight.contiguous().view(torch.uint8), w_e8m0,
+                                  _bias(pw_bias, value.device), True)
     return out.reshape(batch, height, width, n).permute(0, 3, 1, 2)
 
 
 def depthwise5x5_relu_pointwise_int8(value: Tensor, dw_weight: Tensor, dw_bias: Tensor, pw_weight: Tensor,
                                      pw_wscale: Tensor, pw_bias: Tensor, scale: Tensor) -> Tensor:
-    """The INT8 refiner block (``flashim/ops/conv.py:119-138``) -> ``[B, C, H, W]`` view of NHWC BF16: the two-launch
-    composite at every shape. The one-kernel block (``pointwise_int8_fused``) gives the same bits but measured slower
-    on MI355X at 2 x 128 x 400 x 400 (80 against 68-70 us): the INT8 intermediate is 1 byte per element, so the HBM
-    round trip the fusion saves is small, while the composite's producer runs three workgroups per CU against the
-    one-kernel block's two."""
+    """The INT8 refiner block (``flashim/ops/conv.py:119-138``) -> ``[B, C, H, W]`` view of NHWC BF16: one kernel
+    (``fim_depthwise5x5_relu_pointwise_int8``) at 128 x 128 where it is the faster (``_one_kernel_block_wins``),
+    otherwise the two-launch composite (the same bits either way)."""
+    if _fused_pointwise_shape(value, pw_weight) and _one_kernel_block_wins(value):
+        return pointwise_int8_fused(value, dw_weight, dw_bias, pw_weight, pw_wscale, pw_bias, scale)
     return pointwise_int8_composite(value, dw_weight, dw_bias, pw_weight, pw_wscale, pw_bias, scale)
 
 

@@ -40,6 +40,7 @@ struct ConvArgs {
   const uint8_t* w;        // [Cout, T*Cin]
   const int8_t* x_expo;    // MX: [Cin / 32]
   const int8_t* w_expo;    // MX: [Cout, T*Cin / 32]
+  int w_expo_e8m0;         // MX: w_expo holds E8M0 bytes (exponent + 127) instead of signed exponents
   const uint8_t* x_swz;    // MX, per-row scales (XS = 1): E8M0 bytes of x in the 128x4 swizzled layout
   int x_swz_tiles_k;       //   ceil((Cin / 32) / 4)
   const float* a_scale_rows;  // INT8: per-row activation scales [M] (null: the per-tensor a_scale)
@@ -64,6 +65,10 @@ struct ConvArgs {
   int n_tiles, m_tiles;
   int m_base;              // first GEMM row of this launch (a split launch runs its last rows as a second launch)
 };
+
+// The MFMA scale byte (E8M0: exponent + 127) of a weight exponent entry read as int8: signed exponents get + 127,
+// E8M0 bytes pass through; (v + add) & 0xff covers both (an E8M0 byte above 127 reads as v - 256).
+__device__ __forceinline__ int w_scale_byte(const ConvArgs& a, int v) { return (v + (a.w_expo_e8m0 ? 0 : 127)) & 0xff; }
 
 
 constexpr int BM_MAIN = 128;  // pixel rows per tile (the tail of a launch may use 64-row tiles)
@@ -747,7 +752,7 @@ __global__ __launch_bounds__(256, ONE ? 3 : 2) void conv_igemm_kernel(const Conv
     for (int j = 0; j < MB; ++j) sxs[j] = !blk_ok ? 127 : XS ? rsx[j] : rsx[0] + 127;
     int sw[NB];
 #pragma unroll
-    for (int i = 0; i < NB; ++i) sw[i] = blk_ok ? rsw[i] + 127 : 127;
+    for (int i = 0; i < NB; ++i) sw[i] = blk_ok ? w_scale_byte(a, rsw[i]) : 127;
     const uint8_t* st = lds + buf * STAGE;
     if constexpr (KIND == KIND_INT8) {
       v4i xlo[MB], xhi[MB];
@@ -1040,7 +1045,7 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
     if (KIND == KIND_MX) {
       sxs = eok[ec] ? esx[ec] + 127 : 127;
 #pragma unroll
-      for (int i = 0; i < NB; ++i) sw[i] = eok[ec] ? esw[ec][i] + 127 : 127;
+      for (int i = 0; i < NB; ++i) sw[i] = eok[ec] ? w_scale_byte(a, esw[ec][i]) : 127;
     }
     const bool more = kt + NST - 1 < nk;
     __builtin_amdgcn_sched_barrier(0);
@@ -1292,7 +1297,7 @@ __global__ __launch_bounds__(512, 1) void conv_patch_kernel(const ConvArgs a) {
 #pragma unroll
     for (int i = 0; i < WEXP_PASSES; ++i) {
       const int idx = tid + 512 * i;
-      e[i] = idx < WEXP_N && idx < wexp_valid ? (int)a.w_expo[(int64_t)n0 * (TAPS * 4) + idx] + 127 : 127;
+      e[i] = idx < WEXP_N && idx < wexp_valid ? w_scale_byte(a, a.w_expo[(int64_t)n0 * (TAPS * 4) + idx]) : 127;
     }
 #pragma unroll
     for (int i = 0; i < WEXP_PASSES; ++i)
@@ -1617,7 +1622,7 @@ __global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
 #pragma unroll
     for (int i = 0; i < WEXP_PASSES; ++i) {
       const int idx = tid + 512 * i;
-      e[i] = idx < WEXP_N && idx < wexp_valid ? (int)a.w_expo[(int64_t)n0 * (KS * 4) + idx] + 127 : 127;
+      e[i] = idx < WEXP_N && idx < wexp_valid ? w_scale_byte(a, a.w_expo[(int64_t)n0 * (KS * 4) + idx]) : 127;
     }
 #pragma unroll
     for (int i = 0; i < WEXP_PASSES; ++i)
@@ -1938,7 +1943,7 @@ __global__ __launch_bounds__(512, 1) void conv_1x1_resident_kernel(const ConvArg
 #pragma unroll
       for (int i = 0; i < NB; ++i) {
         const int n = min(n0 + wn * (NB * 16) + i * 16 + (lane & 15), a.Cout - 1);
-        sw[st][i] = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(wr, n * cblocks + 4 * st + g, 0, 0) + 127;
+        sw[st][i] = w_scale_byte(a, (int8_t)__builtin_amdgcn_raw_buffer_load_b8(wr, n * cblocks + 4 * st + g, 0, 0));
       }
     }
   }
@@ -2483,8 +2488,8 @@ int fim_int8_linear_quantize(const int8_t* a, int64_t M, int64_t K, const int8_t
 // a [M, K] E4M3 with its E8M0 scales in the 128x4 swizzled layout (a_scale_swizzled), weight [N, K] E4M3 with int8
 // exponents [N, K/32]; out BF16 [M, N] = a @ weight^T (+ bias).
 int fim_mxfp8_scaled_mm(const uint8_t* a, int64_t M, int64_t K, const uint8_t* a_scale_swizzled,
-                        const uint8_t* weight, int64_t N, const int8_t* weight_exponent, const void* bias,
-                        int bias_dtype, void* out, hipStream_t stream) {
+                        const uint8_t* weight, int64_t N, const int8_t* weight_exponent, int weight_scale_e8m0,
+                        const void* bias, int bias_dtype, void* out, hipStream_t stream) {
   if (a == nullptr || a_scale_swizzled == nullptr || weight == nullptr || weight_exponent == nullptr || out == nullptr)
     return FIM_ERR_INVALID;
   if (K % 32 != 0) return FIM_ERR_UNSUPPORTED;
@@ -2496,6 +2501,7 @@ int fim_mxfp8_scaled_mm(const uint8_t* a, int64_t M, int64_t K, const uint8_t* a
   c.x_swz = a_scale_swizzled;
   c.x_swz_tiles_k = (int)(((K / 32) + 3) / 4);
   c.w_expo = weight_exponent;
+  c.w_expo_e8m0 = weight_scale_e8m0 != 0;
   fill_geometry(c, 1, 1, M, K, N, 1, 1, 1, 1, 0, 0, 1, 1);
   fill_epilogue(c, bias, bias_dtype, nullptr, 0, 0, nullptr, 0, 0, out);
   c.out_mode = OUT_BF16;

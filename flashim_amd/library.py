@@ -306,19 +306,20 @@ def int8_linear_quantize_(a: Tensor, weight: Tensor, a_scale: Tensor, w_scale: T
 
 @torch.library.custom_op(f"{NS}::mxfp8_scaled_mm", mutates_args=())
 def mxfp8_scaled_mm(a: Tensor, a_scale_swizzled: Tensor, weight: Tensor, weight_exponent: Tensor,
-                    bias: Optional[Tensor]) -> Tensor:
-    """``a [M, K]`` / ``weight [N, K]``: ``uint8`` views of E4M3; ``a_scale_swizzled`` ``uint8`` E8M0 bytes."""
+                    bias: Optional[Tensor], weight_scale_e8m0: bool = False) -> Tensor:
+    """``a [M, K]`` / ``weight [N, K]``: ``uint8`` views of E4M3; ``a_scale_swizzled`` ``uint8`` E8M0 bytes;
+    ``weight_exponent`` ``[N, K/32]`` int8 exponents, or (``weight_scale_e8m0``) their E8M0 bytes."""
     m, k = a.shape
     n = weight.shape[0]
     out = torch.empty(m, n, device=a.device, dtype=torch.bfloat16)
     _lib.call("fim_mxfp8_scaled_mm", a.data_ptr(), m, k, a_scale_swizzled.data_ptr(), weight.data_ptr(), n,
-              weight_exponent.data_ptr(), _ptr(bias), _bias_code(bias), out.data_ptr(), _stream(a),
-              what=f"mxfp8_scaled_mm {m}x{k} -> {n}")
+              weight_exponent.data_ptr(), int(weight_scale_e8m0), _ptr(bias), _bias_code(bias), out.data_ptr(),
+              _stream(a), what=f"mxfp8_scaled_mm {m}x{k} -> {n}")
     return out
 
 
 @mxfp8_scaled_mm.register_fake
-def _(a, a_scale_swizzled, weight, weight_exponent, bias):
+def _(a, a_scale_swizzled, weight, weight_exponent, bias, weight_scale_e8m0=False):
     return a.new_empty((a.shape[0], weight.shape[0]), dtype=torch.bfloat16)
 
 

@@ -141,11 +141,12 @@ int fim_int8_linear_quantize(const int8_t* a, int64_t M, int64_t K, const int8_t
                              hipStream_t stream);
 
 /* Block-scaled MXFP8 GEMM: a [M, K] E4M3 with per-(row, 32) E8M0 scales in cuBLAS' 128x4 swizzled layout, weight
- * [N, K] E4M3 with int8 exponents [N, K/32] -> BF16 [M, N] (+ bias). Replaces ops.mxfp8_scaled_mm
- * (flashim/ops/gemm.py:40-52; the caller passes b_t^T and unswizzled b exponents). */
+ * [N, K] E4M3 with scales [N, K/32]: int8 exponents (weight_scale_e8m0 0) or their E8M0 bytes, exponent + 127
+ * (weight_scale_e8m0 1, the unswizzled pw_scale_u8 of the refiner-block ops) -> BF16 [M, N] (+ bias). Replaces
+ * ops.mxfp8_scaled_mm (flashim/ops/gemm.py:40-52; the caller passes b_t^T and unswizzled b scales). */
 int fim_mxfp8_scaled_mm(const uint8_t* a, int64_t M, int64_t K, const uint8_t* a_scale_swizzled,
-                        const uint8_t* weight, int64_t N, const int8_t* weight_exponent, const void* bias,
-                        int bias_dtype, void* out, hipStream_t stream);
+                        const uint8_t* weight, int64_t N, const int8_t* weight_exponent, int weight_scale_e8m0,
+                        const void* bias, int bias_dtype, void* out, hipStream_t stream);
 
 /* Fused MLP, C = 64 -> H = 256 -> C = 64 rows of x [P, C] (hidden layer quantized into LDS, never written out).
  * kind 0 INT8 (x_scale, h_scale FP32 scalars; w1_scale FP32 [H], w2_scale FP32 [C]), 1 MXFP8 (x_scale int8 [C/32],

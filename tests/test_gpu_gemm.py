@@ -124,6 +124,14 @@ def test_mxfp8_scaled_mm(m, k, n, has_bias):
     want = ref.mxfp8_scaled_mm(a, b_t, a_scale, b_scale, bias)
     assert got.shape == (m, n) and got.dtype == torch.bfloat16
     _assert_mx_close(got, want)
+    # the weight scales as E8M0 bytes (the refiner-block ops' pw_scale_u8) give the same bits on every kernel
+    b_e8m0 = ref.exponent_to_e8m0(b_exp).view(torch.int8)
+    args = (a.view(torch.uint8).to(DEV), a_scale.view(torch.uint8).to(DEV), b.view(torch.uint8).to(DEV))
+    bias_d = None if bias is None else bias.to(DEV)
+    signed = library.mxfp8_scaled_mm(*args, b_exp.to(torch.int8).to(DEV), bias_d)
+    biased = library.mxfp8_scaled_mm(*args, b_e8m0.to(DEV), bias_d, True)
+    assert torch.equal(signed.view(torch.int16), biased.view(torch.int16))
+    assert torch.equal(signed.cpu().view(torch.int16), got.view(torch.int16))
 
 
 IM2COL = [
@@ -159,7 +167,8 @@ def _block_inputs(batch, channels, hw, seed):
     return x, dw_w, dw_b, pw_b, g
 
 
-@pytest.mark.parametrize("batch,channels,hw", [(2, 64, (20, 30)), (1, 128, (33, 17)), (2, 32, (5, 7))])
+# (1, 128, (256, 256)): 256 tiles of the one-kernel block, inside its band on 256 CUs (the op takes the one kernel)
+@pytest.mark.parametrize("batch,channels,hw", [(2, 64, (20, 30)), (1, 128, (33, 17)), (2, 32, (5, 7)), (1, 128, (256, 256))])
 def test_depthwise_pointwise_int8(batch, channels, hw):
     x, dw_w, dw_b, pw_b, g = _block_inputs(batch, channels, hw, seed=channels)
     pw_w = torch.randint(-127, 128, (channels, channels), dtype=torch.int8, generator=g)
@@ -177,7 +186,8 @@ def test_depthwise_pointwise_int8(batch, channels, hw):
     assert rel < 1e-2
 
 
-@pytest.mark.parametrize("batch,channels,hw", [(2, 64, (20, 30)), (1, 128, (33, 17)), (2, 32, (5, 7))])
+# (1, 128, (256, 256)): 256 tiles of the one-kernel block, inside its band on 256 CUs (the op takes the one kernel)
+@pytest.mark.parametrize("batch,channels,hw", [(2, 64, (20, 30)), (1, 128, (33, 17)), (2, 32, (5, 7)), (1, 128, (256, 256))])
 def test_depthwise_pointwise_mxfp8(batch, channels, hw):
     x, dw_w, dw_b, pw_b, g = _block_inputs(batch, channels, hw, seed=channels + 1)
     pw_w, pw_e = ref.quantized_weight_from_float(torch.randn(channels, channels, generator=g) * 0.1)
