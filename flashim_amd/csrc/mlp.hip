@@ -48,13 +48,21 @@ __device__ __forceinline__ float load_bias(const void* b, int dtype, int i) {
   return dtype == FIM_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(b)[i]) : static_cast<const float*>(b)[i];
 }
 
+// Workgroups per CU: three (51.5 KB of LDS each, the input tile sharing the hidden tile's space) when the kernel fits
+// 168 VGPRs, else two.
+template <int KIND>
+constexpr int mlp_wgs_per_cu() { return KIND == MLP_INT8 ? 3 : 2; }
+
 template <int KIND, int SEM>
-__global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
+__global__ __launch_bounds__(256, mlp_wgs_per_cu<KIND>()) void refiner_mlp_kernel(const MlpArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t w1s[MLP_H * MLP_C];  // [h][64 B]
   __shared__ __attribute__((aligned(16))) uint8_t w2s[MLP_C * MLP_H];  // [c][256 B]
-  __shared__ __attribute__((aligned(16))) uint8_t xs[MLP_BM * MLP_C];  // [px][64 B]
   __shared__ __attribute__((aligned(16))) uint8_t hs[MLP_BM * MLP_H];  // [px][256 B]
-  __shared__ float b1s[MLP_H], b2s[MLP_C], s1[MLP_H], s2[MLP_C], hsc[MLP_H];  // hsc: MX hidden scale 2^e
+  // the input tile [px][64 B] lives in the hidden tile's first 4 KB: read into registers at the start of the expand,
+  // before any hidden value is written (a barrier between), and written again after the contract's reads (a barrier
+  // before)
+  uint8_t* const xs = hs;
+  __shared__ float b1s[MLP_H], b2s[MLP_C], s1[MLP_H], s2[MLP_C];
   __shared__ int8_t e1s[MLP_H * (MLP_C / 32)], e2s[MLP_C * (MLP_H / 32)];
 
   const int tid = threadIdx.x;
@@ -80,7 +88,6 @@ __global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
     if (KIND == MLP_INT8) {
       s1[h] = *static_cast<const float*>(a.x_scale) * static_cast<const float*>(a.w1_scale)[h];
     } else {
-      hsc[h] = exp2_int((int)static_cast<const int8_t*>(a.h_scale)[h >> 5]);
       e1s[2 * h] = static_cast<const int8_t*>(a.w1_scale)[2 * h];
       e1s[2 * h + 1] = static_cast<const int8_t*>(a.w1_scale)[2 * h + 1];
     }
@@ -105,6 +112,12 @@ __global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
     hq_inv = __fdiv_rn(1.0f, hq_scale);
   }
   const int8_t* hexp = static_cast<const int8_t*>(a.h_scale);
+  // MX: the scales 2^e of this wave's two 32-channel hidden blocks (2 wave, 2 wave + 1)
+  float hsc_w[2] = {1.0f, 1.0f};
+  if (KIND == MLP_MX) {
+    hsc_w[0] = exp2_int((int)hexp[2 * __builtin_amdgcn_readfirstlane(wave)]);
+    hsc_w[1] = exp2_int((int)hexp[2 * __builtin_amdgcn_readfirstlane(wave) + 1]);
+  }
 
   // per-lane pieces of the tile loop
   const int ld_px = tid >> 2, ld_seg = tid & 3;  // the input segment this lane stages
@@ -133,8 +146,9 @@ __global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
 
   for (int t = blockIdx.x; t < a.ntiles; t += gridDim.x) {
     const int px0 = t * MLP_BM;
+    __syncthreads();  // the previous tile's contract is done reading the hidden tile (the input tile's space)
     *reinterpret_cast<uint4*>(&xs[ld_dst]) = cur;
-    __syncthreads();  // input tile staged; the previous tile's hidden reads are done
+    __syncthreads();  // input tile staged
     cur = load_tile(t + gridDim.x);  // prefetch the next tile's input and residual
     load_res(t + gridDim.x, res_nxt);
 
@@ -179,12 +193,13 @@ __global__ __launch_bounds__(256, 2) void refiner_mlp_kernel(const MlpArgs a) {
         }
       }
       __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();  // every wave holds its input fragments: the hidden tile may be written over the input tile
 #pragma unroll
       for (int ib = 0; ib < 2; ++ib) {
         const int hb = 64 * wave + 32 * ib + 4 * h2;  // hidden channel of register 0; register r adds 8 (r / 4) + r % 4
         // MXFP8: the block's scale; GELU outputs are >= -0.1700 (BF16), so the lower clamp at -448 * 2^e is a no-op
         // for every scale >= 2^-11 (wave-uniform: the wave's 32 channels share one scale block)
-        const float sc = KIND == MLP_MX ? hsc[hb] : 1.0f, bound = 448.0f * sc;
+        const float sc = hsc_w[ib], bound = 448.0f * sc;
         const bool two_sided = __builtin_amdgcn_readfirstlane((int)(sc < 0x1p-11f)) != 0;
 #pragma unroll
         for (int jb = 0; jb < 2; ++jb) {
@@ -326,7 +341,9 @@ extern "C" int fim_refiner_mlp(int kind, int semantics, const uint8_t* x, int64_
   if (P == 0) return FIM_OK;
   MlpArgs a{x, w1, w2, x_scale, w1_scale, h_scale, w2_scale, b1, b1_dtype, b2, b2_dtype, residual, out, (int)P, 0};
   a.ntiles = (int)cdiv(P, MLP_BM);
-  const int grid = a.ntiles < 512 ? a.ntiles : 512;  // two workgroups per CU, grid-stride over the tiles
+  // grid-stride over the tiles with as many workgroups as fit on the GPU at once
+  const int slots = device_cus() * (kind == MLP_INT8 ? mlp_wgs_per_cu<MLP_INT8>() : mlp_wgs_per_cu<MLP_MX>());
+  const int grid = a.ntiles < slots ? a.ntiles : slots;
   if (kind == MLP_INT8)
     refiner_mlp_kernel<MLP_INT8, MLP_BLOCK><<<dim3(grid), dim3(256), 0, stream>>>(a);
   else if (semantics == MLP_BLOCK)
