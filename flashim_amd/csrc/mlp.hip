@@ -50,11 +50,14 @@ __device__ __forceinline__ float load_bias(const void* b, int dtype, int i) {
 
 // Workgroups per CU: three (51.5 KB of LDS each, the input tile sharing the hidden tile's space) when the kernel fits
 // 168 VGPRs, else two.
+template <int KIND, int SEM>
+constexpr int mlp_wgs_per_cu() { return KIND == MLP_MX && SEM == MLP_REFERENCE ? 2 : 3; }  // (the latter spills at 3)
+// MXFP8 (182 VGPRs with all four accumulator blocks live) computes and drains one hidden block at a time
 template <int KIND>
-constexpr int mlp_wgs_per_cu() { return KIND == MLP_INT8 ? 3 : 2; }
+constexpr bool mlp_split_expand() { return KIND == MLP_MX; }
 
 template <int KIND, int SEM>
-__global__ __launch_bounds__(256, mlp_wgs_per_cu<KIND>()) void refiner_mlp_kernel(const MlpArgs a) {
+__global__ __launch_bounds__(256, (mlp_wgs_per_cu<KIND, SEM>())) void refiner_mlp_kernel(const MlpArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t w1s[MLP_H * MLP_C];  // [h][64 B]
   __shared__ __attribute__((aligned(16))) uint8_t w2s[MLP_C * MLP_H];  // [c][256 B]
   __shared__ __attribute__((aligned(16))) uint8_t hs[MLP_BM * MLP_H];  // [px][256 B]
@@ -170,82 +173,164 @@ __global__ __launch_bounds__(256, mlp_wgs_per_cu<KIND>()) void refiner_mlp_kerne
         xlo[jb] = *reinterpret_cast<const v4i*>(&xs[row * MLP_C + ((h2 ^ ((row >> 2) & 3)) << 4)]);
         xhi[jb] = *reinterpret_cast<const v4i*>(&xs[row * MLP_C + (((2 + h2) ^ ((row >> 2) & 3)) << 4)]);
       }
-      v16i acc_i[2][2];
-      v16f acc_f[2][2];
+      if constexpr (mlp_split_expand<KIND>()) {
+        // one hidden block's MFMAs, then its epilogue: half the accumulators are live at a time, which fits the
+        // registers of three workgroups per CU (the other workgroups' waves cover the MFMA latency)
+        v16i acc_i[2][2];
+        v16f acc_f[2][2];
+        __syncthreads();  // every wave holds its input fragments: the hidden tile may be written over the input tile
 #pragma unroll
-      for (int ib = 0; ib < 2; ++ib) {
-        const int h = 64 * wave + 32 * ib + l32;
-        const v4i wlo = *reinterpret_cast<const v4i*>(&w1s[h * MLP_C + ((h2 ^ ((h >> 2) & 3)) << 4)]);
-        const v4i whi = *reinterpret_cast<const v4i*>(&w1s[h * MLP_C + (((2 + h2) ^ ((h >> 2) & 3)) << 4)]);
-        const int sw = (int)e1s[2 * h + h2] + 127;
+        for (int ib = 0; ib < 2; ++ib) {
+          const int h = 64 * wave + 32 * ib + l32;
+          const v4i wlo = *reinterpret_cast<const v4i*>(&w1s[h * MLP_C + ((h2 ^ ((h >> 2) & 3)) << 4)]);
+          const v4i whi = *reinterpret_cast<const v4i*>(&w1s[h * MLP_C + (((2 + h2) ^ ((h >> 2) & 3)) << 4)]);
+          const int sw = (int)e1s[2 * h + h2] + 127;
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb) {
-          if (KIND == MLP_INT8) {
-            v16i c = {};
-            c = __builtin_amdgcn_mfma_i32_32x32x32_i8(wlo, xlo[jb], c, 0, 0, 0);
-            acc_i[ib][jb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(whi, xhi[jb], c, 0, 0, 0);
-          } else {
-            const v8i wa = __builtin_shufflevector(wlo, whi, 0, 1, 2, 3, 4, 5, 6, 7);
-            const v8i xb = __builtin_shufflevector(xlo[jb], xhi[jb], 0, 1, 2, 3, 4, 5, 6, 7);
-            acc_f[ib][jb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wa, xb, v16f{}, 0, 0, 0, sw, 0,
-                                                                            xe[h2] + 127);
-          }
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      __syncthreads();  // every wave holds its input fragments: the hidden tile may be written over the input tile
-#pragma unroll
-      for (int ib = 0; ib < 2; ++ib) {
-        const int hb = 64 * wave + 32 * ib + 4 * h2;  // hidden channel of register 0; register r adds 8 (r / 4) + r % 4
-        // MXFP8: the block's scale; GELU outputs are >= -0.1700 (BF16), so the lower clamp at -448 * 2^e is a no-op
-        // for every scale >= 2^-11 (wave-uniform: the wave's 32 channels share one scale block)
-        const float sc = hsc_w[ib], bound = 448.0f * sc;
-        const bool two_sided = __builtin_amdgcn_readfirstlane((int)(sc < 0x1p-11f)) != 0;
-#pragma unroll
-        for (int jb = 0; jb < 2; ++jb) {
-          float yb[16];  // the block's 16 values, all computed before any is quantized (one INT8 tie test)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int hh = hb + 8 * (r >> 2) + (r & 3);
-            float y;
+          for (int jb = 0; jb < 2; ++jb) {
             if (KIND == MLP_INT8) {
-              y = __fadd_rn(__fmul_rn((float)acc_i[ib][jb][r], s1[hh]), b1s[hh]);
-            } else if (SEM == MLP_REFERENCE) {  // bf16(x W1^T), + b1 in FP32, GELU of the FP32 sum
-              y = __fadd_rn(round_bf16_hw(acc_f[ib][jb][r]), b1s[hh]);
+              v16i c = {};
+              c = __builtin_amdgcn_mfma_i32_32x32x32_i8(wlo, xlo[jb], c, 0, 0, 0);
+              acc_i[ib][jb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(whi, xhi[jb], c, 0, 0, 0);
             } else {
-              y = __fadd_rn(acc_f[ib][jb][r], b1s[hh]);
+              const v8i wa = __builtin_shufflevector(wlo, whi, 0, 1, 2, 3, 4, 5, 6, 7);
+              const v8i xb = __builtin_shufflevector(xlo[jb], xhi[jb], 0, 1, 2, 3, 4, 5, 6, 7);
+              acc_f[ib][jb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wa, xb, v16f{}, 0, 0, 0, sw, 0,
+                                                                              xe[h2] + 127);
             }
-            yb[r] = SEM == MLP_BLOCK ? round_bf16_hw(y) : y;  // the conv epilogue: BF16 rounding before the GELU
           }
-          gelu_erf_n<16>(yb);  // the block's 16 GELU chains interleaved
-          uint32_t qw[4];
-          if (KIND == MLP_MX) {  // BF16 rounding and static E4M3 in one step
+
+          const int hb = 64 * wave + 32 * ib + 4 * h2;  // hidden channel of register 0; register r adds 8 (r / 4) + r % 4
+          // MXFP8: the block's scale; GELU outputs are >= -0.1700 (BF16), so the lower clamp at -448 * 2^e is a no-op
+          // for every scale >= 2^-11 (wave-uniform: the wave's 32 channels share one scale block)
+          const float sc = hsc_w[ib], bound = 448.0f * sc;
+          const bool two_sided = __builtin_amdgcn_readfirstlane((int)(sc < 0x1p-11f)) != 0;
+#pragma unroll
+          for (int jb = 0; jb < 2; ++jb) {
+            float yb[16];  // the block's 16 values, all computed before any is quantized (one INT8 tie test)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int hh = hb + 8 * (r >> 2) + (r & 3);
+              float y;
+              if (KIND == MLP_INT8) {
+                y = __fadd_rn(__fmul_rn((float)acc_i[ib][jb][r], s1[hh]), b1s[hh]);
+              } else if (SEM == MLP_REFERENCE) {  // bf16(x W1^T), + b1 in FP32, GELU of the FP32 sum
+                y = __fadd_rn(round_bf16_hw(acc_f[ib][jb][r]), b1s[hh]);
+              } else {
+                y = __fadd_rn(acc_f[ib][jb][r], b1s[hh]);
+              }
+              yb[r] = SEM == MLP_BLOCK ? round_bf16_hw(y) : y;  // the conv epilogue: BF16 rounding before the GELU
+            }
+            gelu_erf_n<16>(yb);  // the block's 16 GELU chains interleaved
+            uint32_t qw[4];
+            if (KIND == MLP_MX) {  // BF16 rounding and static E4M3 in one step
+#pragma unroll
+              for (int k = 0; k < 4; ++k) {
+                float q[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) q[v] = __builtin_elementwise_minimum(yb[4 * k + v], bound);
+                if (two_sided) {
+#pragma unroll
+                  for (int v = 0; v < 4; ++v) q[v] = __builtin_elementwise_maximum(q[v], -bound);
+                }
+                qw[k] = e4m3x4_of_bf16_inrange(q[0], q[1], q[2], q[3], sc);
+              }
+            } else {
+#pragma unroll
+              for (int r = 0; r < 16; ++r) yb[r] = round_bf16_hw(yb[r]);
+              int qi[16];
+              quantize_int8_fast_n<16>(yb, hq_scale, hq_inv, qi);
+#pragma unroll
+              for (int k = 0; k < 4; ++k)
+                qw[k] = (uint32_t)(uint8_t)qi[4 * k] | ((uint32_t)(uint8_t)qi[4 * k + 1] << 8) |
+                        ((uint32_t)(uint8_t)qi[4 * k + 2] << 16) | ((uint32_t)(uint8_t)qi[4 * k + 3] << 24);
+            }
+            const int px = 32 * jb + l32;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-              float q[4];
-#pragma unroll
-              for (int v = 0; v < 4; ++v) q[v] = __builtin_elementwise_minimum(yb[4 * k + v], bound);
-              if (two_sided) {
-#pragma unroll
-                for (int v = 0; v < 4; ++v) q[v] = __builtin_elementwise_maximum(q[v], -bound);
-              }
-              qw[k] = e4m3x4_of_bf16_inrange(q[0], q[1], q[2], q[3], sc);
+              const int h0 = hb + 8 * k;
+              *reinterpret_cast<uint32_t*>(&hs[px * MLP_H + ((((h0 >> 4)) ^ (px & 15)) << 4) + (h0 & 15)]) = qw[k];
             }
-          } else {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) yb[r] = round_bf16_hw(yb[r]);
-            int qi[16];
-            quantize_int8_fast_n<16>(yb, hq_scale, hq_inv, qi);
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-              qw[k] = (uint32_t)(uint8_t)qi[4 * k] | ((uint32_t)(uint8_t)qi[4 * k + 1] << 8) |
-                      ((uint32_t)(uint8_t)qi[4 * k + 2] << 16) | ((uint32_t)(uint8_t)qi[4 * k + 3] << 24);
           }
-          const int px = 32 * jb + l32;
+
+        }
+      } else {
+        v16i acc_i[2][2];
+        v16f acc_f[2][2];
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const int h0 = hb + 8 * k;
-            *reinterpret_cast<uint32_t*>(&hs[px * MLP_H + ((((h0 >> 4)) ^ (px & 15)) << 4) + (h0 & 15)]) = qw[k];
+        for (int ib = 0; ib < 2; ++ib) {
+          const int h = 64 * wave + 32 * ib + l32;
+          const v4i wlo = *reinterpret_cast<const v4i*>(&w1s[h * MLP_C + ((h2 ^ ((h >> 2) & 3)) << 4)]);
+          const v4i whi = *reinterpret_cast<const v4i*>(&w1s[h * MLP_C + (((2 + h2) ^ ((h >> 2) & 3)) << 4)]);
+          const int sw = (int)e1s[2 * h + h2] + 127;
+#pragma unroll
+          for (int jb = 0; jb < 2; ++jb) {
+            if (KIND == MLP_INT8) {
+              v16i c = {};
+              c = __builtin_amdgcn_mfma_i32_32x32x32_i8(wlo, xlo[jb], c, 0, 0, 0);
+              acc_i[ib][jb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(whi, xhi[jb], c, 0, 0, 0);
+            } else {
+              const v8i wa = __builtin_shufflevector(wlo, whi, 0, 1, 2, 3, 4, 5, 6, 7);
+              const v8i xb = __builtin_shufflevector(xlo[jb], xhi[jb], 0, 1, 2, 3, 4, 5, 6, 7);
+              acc_f[ib][jb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wa, xb, v16f{}, 0, 0, 0, sw, 0,
+                                                                              xe[h2] + 127);
+            }
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();  // every wave holds its input fragments: the hidden tile may be written over the input tile
+#pragma unroll
+        for (int ib = 0; ib < 2; ++ib) {
+          const int hb = 64 * wave + 32 * ib + 4 * h2;  // hidden channel of register 0; register r adds 8 (r / 4) + r % 4
+          // MXFP8: the block's scale; GELU outputs are >= -0.1700 (BF16), so the lower clamp at -448 * 2^e is a no-op
+          // for every scale >= 2^-11 (wave-uniform: the wave's 32 channels share one scale block)
+          const float sc = hsc_w[ib], bound = 448.0f * sc;
+          const bool two_sided = __builtin_amdgcn_readfirstlane((int)(sc < 0x1p-11f)) != 0;
+#pragma unroll
+          for (int jb = 0; jb < 2; ++jb) {
+            float yb[16];  // the block's 16 values, all computed before any is quantized (one INT8 tie test)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int hh = hb + 8 * (r >> 2) + (r & 3);
+              float y;
+              if (KIND == MLP_INT8) {
+                y = __fadd_rn(__fmul_rn((float)acc_i[ib][jb][r], s1[hh]), b1s[hh]);
+              } else if (SEM == MLP_REFERENCE) {  // bf16(x W1^T), + b1 in FP32, GELU of the FP32 sum
+                y = __fadd_rn(round_bf16_hw(acc_f[ib][jb][r]), b1s[hh]);
+              } else {
+                y = __fadd_rn(acc_f[ib][jb][r], b1s[hh]);
+              }
+              yb[r] = SEM == MLP_BLOCK ? round_bf16_hw(y) : y;  // the conv epilogue: BF16 rounding before the GELU
+            }
+            gelu_erf_n<16>(yb);  // the block's 16 GELU chains interleaved
+            uint32_t qw[4];
+            if (KIND == MLP_MX) {  // BF16 rounding and static E4M3 in one step
+#pragma unroll
+              for (int k = 0; k < 4; ++k) {
+                float q[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) q[v] = __builtin_elementwise_minimum(yb[4 * k + v], bound);
+                if (two_sided) {
+#pragma unroll
+                  for (int v = 0; v < 4; ++v) q[v] = __builtin_elementwise_maximum(q[v], -bound);
+                }
+                qw[k] = e4m3x4_of_bf16_inrange(q[0], q[1], q[2], q[3], sc);
+              }
+            } else {
+#pragma unroll
+              for (int r = 0; r < 16; ++r) yb[r] = round_bf16_hw(yb[r]);
+              int qi[16];
+              quantize_int8_fast_n<16>(yb, hq_scale, hq_inv, qi);
+#pragma unroll
+              for (int k = 0; k < 4; ++k)
+                qw[k] = (uint32_t)(uint8_t)qi[4 * k] | ((uint32_t)(uint8_t)qi[4 * k + 1] << 8) |
+                        ((uint32_t)(uint8_t)qi[4 * k + 2] << 16) | ((uint32_t)(uint8_t)qi[4 * k + 3] << 24);
+            }
+            const int px = 32 * jb + l32;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              const int h0 = hb + 8 * k;
+              *reinterpret_cast<uint32_t*>(&hs[px * MLP_H + ((((h0 >> 4)) ^ (px & 15)) << 4) + (h0 & 15)]) = qw[k];
+            }
           }
         }
       }
@@ -342,7 +427,9 @@ extern "C" int fim_refiner_mlp(int kind, int semantics, const uint8_t* x, int64_
   MlpArgs a{x, w1, w2, x_scale, w1_scale, h_scale, w2_scale, b1, b1_dtype, b2, b2_dtype, residual, out, (int)P, 0};
   a.ntiles = (int)cdiv(P, MLP_BM);
   // grid-stride over the tiles with as many workgroups as fit on the GPU at once
-  const int slots = device_cus() * (kind == MLP_INT8 ? mlp_wgs_per_cu<MLP_INT8>() : mlp_wgs_per_cu<MLP_MX>());
+  const int slots = device_cus() * (kind == MLP_INT8         ? mlp_wgs_per_cu<MLP_INT8, MLP_BLOCK>()
+                                    : semantics == MLP_BLOCK ? mlp_wgs_per_cu<MLP_MX, MLP_BLOCK>()
+                                                             : mlp_wgs_per_cu<MLP_MX, MLP_REFERENCE>());
   const int grid = a.ntiles < slots ? a.ntiles : slots;
   if (kind == MLP_INT8)
     refiner_mlp_kernel<MLP_INT8, MLP_BLOCK><<<dim3(grid), dim3(256), 0, stream>>>(a);
