@@ -97,6 +97,31 @@ def test_int8_conv2d_config1():
     assert torch.equal(got, ref.int8_conv2d(x, wq, a_scale, w_scale, bias, *geo))
 
 
+# small 3x3 stride-1 convs with Cin = 64 and an output width that is a multiple of 64 run on the one-load-phase
+# row-segment kernel: images at the top and bottom and both side edges, two images, two N tiles, a partial last N
+# tile is not allowed (Cout % 64), so 128 output channels; the shapes stay below one 128-row tile per CU (256 CUs)
+ROW3_CASES = [((1, 7, 64), 64), ((2, 5, 128), 64), ((1, 9, 192), 128), ((1, 128, 128), 64)]
+
+
+@pytest.mark.parametrize("case", range(len(ROW3_CASES)))
+def test_int8_conv2d_row_segment_kernel(case):
+    """Bit-exact BF16 out (bias, ReLU), with a residual, and INT8 out, against the oracle."""
+    shape, cout = ROW3_CASES[case]
+    geo = (3, 3, 1, 1, 1, 1, 1, 1)
+    x, weight, a_scale, w_scale, bias = _int8_inputs(64, cout, 3, 3, True, shape=shape)
+    args = _dev(x, weight, a_scale, w_scale, bias)
+    hip = ops.int8_conv2d.get("hip")
+    for relu in (False, True):
+        got = hip(*args, *geo, relu=relu).cpu()
+        assert torch.equal(got, ref.int8_conv2d(x, weight, a_scale, w_scale, bias, *geo, relu=relu)), (case, relu)
+    res = (torch.randn(*shape, cout) * 4).to(torch.bfloat16)
+    got_r = hip(*args, *geo, relu=True, residual=res.to(DEV)).cpu()
+    assert torch.equal(got_r, ref.int8_conv2d(x, weight, a_scale, w_scale, bias, *geo, relu=True, residual=res)), case
+    out_scale = torch.tensor(0.09)
+    got_q = hip(*args, *geo, out_scale=out_scale.to(DEV)).cpu()
+    assert torch.equal(got_q, ref.int8_conv2d(x, weight, a_scale, w_scale, bias, *geo, out_scale=out_scale)), case
+
+
 @pytest.mark.parametrize("relu", [False, True])
 @pytest.mark.parametrize("gelu", [False, True])
 def test_int8_conv2d_epilogues(relu, gelu):
