@@ -2202,33 +2202,35 @@ static int wide_wm(const ConvArgs& a, int lw) {
 }
 
 // Small 3x3 INT8 convs (config 1: 1 x 128 x 128, 64 -> 64): stride 1, pad 1, Cin = 64, output width a multiple of 64,
-// too few 128-row tiles to fill the CUs. A workgroup takes 64 consecutive output pixels (one row segment) x 64 output
-// channels and loads everything it needs in one phase: the 3 x 66-pixel input patch (12.7 KB, zeros outside the
-// image) and the N tile's whole weight (64 rows x 576 B, 37 KB), then runs the 9 taps from LDS (one
-// v_mfma_i32_16x16x64_i8 per tap and 16 x 16 block: wave w takes pixels 16 w .. 16 w + 15 x all 64 channels) and the
-// shared epilogue. Against the 64 x 64 tile kernel's five dependent K steps (each a round trip to L2), there is one
+// too few 128-row tiles to fill the CUs. A workgroup takes 64 consecutive output pixels (one row segment) x R3_TN
+// output channels and loads everything it needs in one phase: the 3 x 66-pixel input patch (12.7 KB, zeros outside
+// the image) and the N tile's whole weight (R3_TN rows x 576 B), then runs the 9 taps from LDS (one
+// v_mfma_i32_16x16x64_i8 per tap and 16 x 16 block: wave w takes pixels 16 w .. 16 w + 15 x all the tile's channels)
+// and the shared epilogue. Against the 64 x 64 tile kernel's five dependent K steps (each a round trip to L2), there is one
 // load latency per workgroup. INT8 sums are exact, so the tap order does not change the result.
 constexpr int R3_TW = 64, R3_CIN = 64, R3_PW = R3_TW + 2;
-constexpr int R3_WROW = 9 * R3_CIN + 16;  // LDS bytes per weight row: 576 + 16 (rows 148 dwords apart: conflict-free)
+constexpr int R3_WROW = 9 * R3_CIN + 16;
+constexpr int R3_TN = 32;  // output channels per workgroup (32 measured 5.26 us on config 1, 64 5.63, 16 5.51)  // LDS bytes per weight row: 576 + 16 (rows 148 dwords apart: conflict-free)
 
-template <int OUT>
+template <int OUT, int TN = R3_TN>
 __global__ __launch_bounds__(256) void conv3x3_row_kernel(const ConvArgs a) {
+  constexpr int NB = TN / 16;
   __shared__ __attribute__((aligned(16))) uint8_t patch[3 * R3_PW * R3_CIN];  // [row][col][64 B], 16-byte slots swizzled
-  __shared__ __attribute__((aligned(16))) uint8_t wt[64 * R3_WROW];           // [n][tap][64 B]
-  __shared__ __attribute__((aligned(16))) float ep_scale[64], ep_bias[64], ep_osc[64];
+  __shared__ __attribute__((aligned(16))) uint8_t wt[TN * R3_WROW];           // [n][tap][64 B]
+  __shared__ __attribute__((aligned(16))) float ep_scale[TN], ep_bias[TN], ep_osc[TN];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, r16 = lane & 15;
   const int per_xcd = gridDim.x >> 3;
   const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
   if (t >= a.n_tiles * a.m_tiles) return;
-  const int n0 = (t % a.n_tiles) * 64;
+  const int n0 = (t % a.n_tiles) * TN;
   const int m0 = (t / a.n_tiles) * R3_TW;
   const int hw = a.Ho * a.Wo;
   const int img = m0 / hw, oh = (m0 - img * hw) / a.Wo, ow0 = m0 - img * hw - oh * a.Wo;
 
   // one load phase: the patch (792 16-byte units) and the weight tile (2304 units), all in flight together
-  constexpr int PU = 3 * R3_PW * 4, WU = 64 * 36;
-  uint4 pv[(PU + 255) / 256], wv[WU / 256];
+  constexpr int PU = 3 * R3_PW * 4, WU = TN * 36;
+  uint4 pv[(PU + 255) / 256], wv[(WU + 255) / 256];
 #pragma unroll
   for (int i = 0; i < (PU + 255) / 256; ++i) {
     const int u = tid + 256 * i;
@@ -2239,13 +2241,14 @@ __global__ __launch_bounds__(256) void conv3x3_row_kernel(const ConvArgs a) {
                : make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
-  for (int i = 0; i < WU / 256; ++i) {
+  for (int i = 0; i < (WU + 255) / 256; ++i) {
     const int u = tid + 256 * i;
     const int n = u / 36, s = u - n * 36;
-    wv[i] = n0 + n < a.Cout ? *reinterpret_cast<const uint4*>(a.w + (int64_t)(n0 + n) * (9 * R3_CIN) + s * 16)
-                            : make_uint4(0, 0, 0, 0);
+    wv[i] = u < WU && n0 + n < a.Cout
+                ? *reinterpret_cast<const uint4*>(a.w + (int64_t)(n0 + n) * (9 * R3_CIN) + s * 16)
+                : make_uint4(0, 0, 0, 0);
   }
-  if (tid < 64) {
+  if (tid < TN) {
     const int n = n0 + tid;
     const bool nok = n < a.Cout;
     ep_scale[tid] = nok ? *a.a_scale * a.w_scale[n] : 1.0f;
@@ -2264,17 +2267,17 @@ __global__ __launch_bounds__(256) void conv3x3_row_kernel(const ConvArgs a) {
       *reinterpret_cast<uint4*>(&patch[(r * R3_PW + col) * R3_CIN + ((seg ^ ((col >> 2) & 3)) << 4)]) = pv[i];
   }
 #pragma unroll
-  for (int i = 0; i < WU / 256; ++i) {
+  for (int i = 0; i < (WU + 255) / 256; ++i) {
     const int u = tid + 256 * i;
     const int n = u / 36, s = u - n * 36;
-    *reinterpret_cast<uint4*>(&wt[n * R3_WROW + s * 16]) = wv[i];
+    if (u < WU) *reinterpret_cast<uint4*>(&wt[n * R3_WROW + s * 16]) = wv[i];
   }
   __syncthreads();
 
-  v4i acc_i[4][1];
-  v4f acc_f[4][1];
+  v4i acc_i[NB][1];
+  v4f acc_f[NB][1];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NB; ++i) {
     acc_i[i][0] = v4i{0, 0, 0, 0};
     acc_f[i][0] = v4f{0.f, 0.f, 0.f, 0.f};
   }
@@ -2286,12 +2289,12 @@ __global__ __launch_bounds__(256) void conv3x3_row_kernel(const ConvArgs a) {
       const v4i xf = *reinterpret_cast<const v4i*>(&patch[(ky * R3_PW + col) * R3_CIN + ((g ^ ((col >> 2) & 3)) << 4)]);
       const int tap = ky * 3 + kx;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < NB; ++i) {
         const v4i wf = *reinterpret_cast<const v4i*>(&wt[(16 * i + r16) * R3_WROW + tap * R3_CIN + 16 * g]);
         acc_i[i][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf, xf, acc_i[i][0], 0, 0, 0);
       }
     }
-  conv_epilogue<KIND_INT8, OUT, 0, 1, 4>(a, acc_i, acc_f, m0 + 16 * wave, n0, 0, ep_scale, ep_bias, ep_osc);
+  conv_epilogue<KIND_INT8, OUT, 0, 1, NB>(a, acc_i, acc_f, m0 + 16 * wave, n0, 0, ep_scale, ep_bias, ep_osc);
 }
 
 // Whether conv3x3_row_kernel takes this launch (see there); the caller has established that the 128-row tiles would
@@ -2299,7 +2302,7 @@ __global__ __launch_bounds__(256) void conv3x3_row_kernel(const ConvArgs a) {
 template <int KIND>
 static bool row3_ok(const ConvArgs& a, int lw) {
   return KIND == KIND_INT8 && lw == 16 && a.kh == 3 && a.kw == 3 && a.sh == 1 && a.sw == 1 && a.ph == 1 && a.pw == 1 &&
-         a.dh == 1 && a.dw == 1 && a.Cin == R3_CIN && a.Wo % R3_TW == 0 && a.Cout % 64 == 0 && a.x_swz == nullptr &&
+         a.dh == 1 && a.dw == 1 && a.Cin == R3_CIN && a.Wo % R3_TW == 0 && a.Cout % R3_TN == 0 && a.x_swz == nullptr &&
          a.a_scale_rows == nullptr && a.pool_out == nullptr && a.out_mode != OUT_E4M3 &&
          (int64_t)a.B * a.H * a.W * R3_CIN < (1LL << 31);
 }
@@ -2360,7 +2363,7 @@ static int launch_conv(ConvArgs a, hipStream_t stream) {
     if (tiles < device_cus()) {
       if (row3_ok<KIND>(a, lw)) {
         ConvArgs t = a;
-        t.n_tiles = a.Cout / 64;
+        t.n_tiles = a.Cout / R3_TN;
         t.m_tiles = a.M / R3_TW;
         const dim3 grid((unsigned)(cdiv((int64_t)t.m_tiles * t.n_tiles, 8) * 8));
         if (a.out_mode == OUT_BF16)

@@ -98,9 +98,9 @@ def test_int8_conv2d_config1():
 
 
 # small 3x3 stride-1 convs with Cin = 64 and an output width that is a multiple of 64 run on the one-load-phase
-# row-segment kernel: images at the top and bottom and both side edges, two images, two N tiles, a partial last N
-# tile is not allowed (Cout % 64), so 128 output channels; the shapes stay below one 128-row tile per CU (256 CUs)
-ROW3_CASES = [((1, 7, 64), 64), ((2, 5, 128), 64), ((1, 9, 192), 128), ((1, 128, 128), 64)]
+# row-segment kernel: images at the top and bottom and both side edges, two images, two to four N tiles of 32
+# channels; the shapes stay below one 128-row tile per CU (256 CUs)
+ROW3_CASES = [((1, 7, 64), 64), ((2, 5, 128), 64), ((1, 9, 192), 128), ((1, 128, 128), 64), ((1, 6, 64), 96)]
 
 
 @pytest.mark.parametrize("case", range(len(ROW3_CASES)))
