@@ -38,7 +38,12 @@ struct DwArgs {
 
 // Tile: 32 output columns x 16 output rows x 32 channels per workgroup (a 1-D grid over (channel slice, column tile,
 // row tile, image), XCD-aware), with the 2-pixel halo of the 5x5 window staged in LDS once.
-constexpr int DW_TW = 32, DW_TH = 16, DW_CS = 32;  // output columns, output rows, channels per workgroup
+// Output columns, output rows, channels per workgroup. 16 columns (a 25.3 KB LDS tile, 74-80 VGPRs: six workgroups per
+// CU) measured faster than 24 (four per CU), 32 (three) and 8 (eight, with 1.5x the halo): config 4 22.9 / 24.8 / 26.8 /
+// 25.0 us, the depthwise-pointwise composites 3-7% faster than at 32.
+constexpr int DW_TW = 16, DW_TH = 16, DW_CS = 32;
+constexpr int DW_CQ = DW_TW / 4;    // 4-column output quads per tile row
+constexpr int DW_SEGS = DW_CQ + 1;  // 4-column staged segments per row (the 2-column halos on both sides)
 
 // ---- The taps on the matrix unit ----------------------------------------------------------------------------
 // v_mfma_f32_4x4x4_16b_bf16 runs 16 independent 4x4x4 products per instruction; each is one channel: D[i][j] (output
@@ -47,22 +52,23 @@ constexpr int DW_TW = 32, DW_TH = 16, DW_CS = 32;  // output columns, output row
 // tile (origin y0 - 2, x0 - 2): 5 weight rows x 2 column segments s = 10 MFMAs per 16 channels x 4 x 4 outputs; the
 // first MFMA of each output block takes the bias as its accumulator input.
 // Operand layout (measured): lane l = 4 b + r supplies A_b[r][0..3] and B_b[0..3][r] and gets D_b[0..3][r].
-// The tile is staged channel-planar ([channel][row][column] BF16, 36 columns per row, planes 360 dwords apart plus 16
+// The tile is staged channel-planar ([channel][row][column] BF16, 20 columns per row, planes 200 dwords apart plus 16
 // dwords per channel octet) so each B operand is one 8-byte LDS read. With 64 four-byte banks and a 64-bit access
-// served 32 lanes at a time, the B reads of 8 channels x 4 rows (plane steps of 40 banks, row steps of 18) and the
-// staging writes (4 octets 16 banks apart, consecutive 4-column groups of a row 2 banks apart) are conflict-free.
-// After the taps each lane activates and quantizes its 64 values in registers (one channel, 4 columns x 8 column
+// served 32 lanes at a time, the B reads of 8 channels x 4 rows (plane steps of 8 banks, row steps of 10: the 4 rows
+// in distinct residues mod 8, the 8 channels apart within each) and the staging writes (4 octets apart by the octet
+// padding, consecutive 4-column groups of a row 2 banks apart) are conflict-free.
+// After the taps each lane activates and quantizes its 32 values in registers (one channel, 4 columns x 4 column
 // quads x 2 rows);
 // static outputs (INT8, static MXFP8, BF16) then go through LDS as finished codes in [row][column][channel] order
 // (byte or 16-bit writes with immediate offsets) and leave as 16-byte stores of 16 (8) channels of one pixel. Dynamic
 // MXFP8 needs the per-(pixel, 32-channel) amax first, so its FP32 values go through LDS in two 8-row halves and a
 // per-pixel pass (8 channels per lane, exponents from 4-lane amax shuffles) quantizes and stores.
-constexpr int DWM_ROWSTR = 18;                      // dwords per staged row (36 columns)
+constexpr int DWM_ROWSTR = 2 * DW_SEGS;              // dwords per staged row (DW_TW + 4 columns)
 constexpr int DWM_PLANE = 20 * DWM_ROWSTR;          // dwords per channel plane
 constexpr int DWM_OCTPAD = 16;                      // extra dwords per channel octet
 constexpr int DWM_LDS = DW_CS * DWM_PLANE + 4 * DWM_OCTPAD;  // 11584 dwords
 __device__ __forceinline__ constexpr int dw_plane(int c) { return c * DWM_PLANE + (c >> 3) * DWM_OCTPAD; }
-constexpr int DWM_UNITS = 20 * 9 * 4;               // staging units: 20 rows x 9 column quads x 4 channel octets
+constexpr int DWM_UNITS = 20 * DW_SEGS * 4;         // staging units: 20 rows x column quads x 4 channel octets
 constexpr int DWM_OROW = DW_TW * DW_CS + 16;        // dwords per staged FP32 output row (dynamic MXFP8, padded)
 constexpr int DWO_ROW8 = DW_TW * DW_CS + 16;        // bytes per staged 8-bit output row (padded: rows 4 banks apart)
 constexpr int DWO_ROW16 = DW_TW * DW_CS * 2 + 16;   // bytes per staged BF16 output row
@@ -89,7 +95,7 @@ __device__ __forceinline__ void dw_stage_unit(uint32_t* sm, int o, int r, int q,
 }
 
 template <int ACT, int OUT>
-__global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
+__global__ __launch_bounds__(256, 6) void dw5x5_mfma_kernel(const DwArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t sm[DWM_LDS];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -144,7 +150,7 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
     for (int j = 0; j < NU; ++j) {
       const int u = min(tid + 256 * j, DWM_UNITS - 1);  // a repeated unit past the end is loaded, not written
       const int o = u & 3, rq = u >> 2;
-      const int r = rq / 9, q = rq - r * 9;
+      const int r = rq / DW_SEGS, q = rq - r * DW_SEGS;
       const int iy = y0 - 2 + r;
       const bool row_ok = iy >= 0 && iy < a.H;
       // byte offsets below 2^31 (the host bounds 40 W C)
@@ -163,26 +169,26 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
     const int u = tid + 256 * j;
     if (j < NU - 1 || u < DWM_UNITS) {
       const int o = u & 3, rq = u >> 2;
-      const int r = rq / 9, q = rq - r * 9;
+      const int r = rq / DW_SEGS, q = rq - r * DW_SEGS;
       dw_stage_unit(sm, o, r, q, v[j]);
     }
   }
 
   __syncthreads();
 
-  // The taps row by row: staged row 8 rh + r4 + rr (rr = 4 t + ky) feeds weight row ky of row quad t; its 9 column
-  // segments (4 columns each) are read once and reused by the 8 column quads x 2 segments, and the next row's
+  // The taps row by row: staged row 8 rh + r4 + rr (rr = 4 t + ky) feeds weight row ky of row quad t; its DW_SEGS column
+  // segments (4 columns each) are read once and reused by the DW_CQ column quads x 2 segments, and the next row's
   // segments are read while this row's MFMAs run.
-  v4f acc[2][8];  // [row quad 2 rh + t][column quad cq]: D[i = 0..3][j = r4]
+  v4f acc[2][DW_CQ];  // [row quad 2 rh + t][column quad cq]: D[i = 0..3][j = r4]
   const uint32_t* plane = &sm[dw_plane(16 * cg + bch) + (8 * rh + r4) * DWM_ROWSTR];
-  uint2 seg[2][9];
+  uint2 seg[2][DW_SEGS];
 #pragma unroll
-  for (int g = 0; g < 9; ++g) seg[0][g] = *reinterpret_cast<const uint2*>(plane + 2 * g);
+  for (int g = 0; g < DW_SEGS; ++g) seg[0][g] = *reinterpret_cast<const uint2*>(plane + 2 * g);
 #pragma unroll
   for (int rr = 0; rr < 9; ++rr) {
     if (rr < 8) {
 #pragma unroll
-      for (int g = 0; g < 9; ++g)
+      for (int g = 0; g < DW_SEGS; ++g)
         seg[(rr + 1) & 1][g] = *reinterpret_cast<const uint2*>(plane + (rr + 1) * DWM_ROWSTR + 2 * g);
     }
 #pragma unroll
@@ -192,7 +198,7 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
 #pragma unroll
       for (int sg = 0; sg < 2; ++sg)
 #pragma unroll
-        for (int cq = 0; cq < 8; ++cq)
+        for (int cq = 0; cq < DW_CQ; ++cq)
           acc[t][cq] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(wa[ky][sg], __builtin_bit_cast(v4bf16, seg[rr & 1][cq + sg]),
                                                               (ky == 0 && sg == 0) ? biasv : acc[t][cq], 0, 0, 0);
     }
@@ -203,11 +209,11 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
 
   if (OUT == DW_MX_DYNAMIC) {
     // ReLU in registers, FP32 values through LDS in two 8-row halves, per-pixel dynamic quantize
-    float y[2][8][4];
+    float y[2][DW_CQ][4];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int cq = 0; cq < 8; ++cq)
+      for (int cq = 0; cq < DW_CQ; ++cq)
 #pragma unroll
         for (int i = 0; i < 4; ++i) y[t][cq][i] = fmaxf(acc[t][cq][i], 0.f);
     const int64_t groups = a.C >> 5;
@@ -215,10 +221,10 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
     const int64_t gi = cbase >> 5;
     float* st = reinterpret_cast<float*>(sm);
     // output pass lanes: 4 consecutive lanes share a pixel (part = 8-channel quarter of the slice); unit tid + 256 it
-    // is tile row 2 it + (tid >> 7) of the half, column (tid >> 2) & 31, so addresses advance by a uniform step per it
-    const int part = tid & 3, col = (tid >> 2) & 31, rl0 = tid >> 7;
-    const int64_t row0 = ((int64_t)b * a.H + y0 + rl0) * a.W + x0 + col;  // output pixel of it = 0, half 0
-    uint8_t* const out0 = static_cast<uint8_t*>(a.out) + row0 * a.C + cbase + 8 * part;
+    // is pixel (tid >> 2) + 64 it of the half (row-major over DW_TW columns); addresses from the tile's first pixel
+    const int part = tid & 3;
+    const int64_t rowt = ((int64_t)b * a.H + y0) * a.W + x0;  // the tile's first output pixel
+    uint8_t* const out0 = static_cast<uint8_t*>(a.out) + rowt * a.C + cbase + 8 * part;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       __syncthreads();  // half 0: the taps are done with the input tile; half 1: the previous output pass is done
@@ -226,16 +232,17 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int cq = 0; cq < 8; ++cq)
+          for (int cq = 0; cq < DW_CQ; ++cq)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
               st[(4 * t + r4) * DWM_OROW + (4 * cq + i) * DW_CS + 16 * cg + bch] = y[t][cq][i];
       }
       __syncthreads();
-      // output pass: 8 rows x 32 columns x 4 parts of 8 channels
+      // output pass: 8 rows x DW_TW columns x 4 parts of 8 channels
 #pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int rl = rl0 + 2 * it;
+      for (int it = 0; it < 8 * DW_TW * 4 / 256; ++it) {
+        const int pxh = (tid >> 2) + 64 * it;
+        const int rl = pxh / DW_TW, col = pxh - rl * DW_TW;
         const int oy = 8 * half + rl;
         const float4 va = *reinterpret_cast<const float4*>(&st[rl * DWM_OROW + col * DW_CS + 8 * part]);
         const float4 vb = *reinterpret_cast<const float4*>(&st[rl * DWM_OROW + col * DW_CS + 8 * part + 4]);
@@ -251,11 +258,11 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
         for (int e = 0; e < 8; ++e) q[e] = __builtin_elementwise_minimum(v[e] * inv, 448.0f);
         const bool ok = interior || (oy < rows && col < cols);
         if (ok) {
-          const int64_t step = (int64_t)(8 * half + 2 * it) * a.W;  // uniform
+          const int64_t step = (int64_t)oy * a.W + col;  // pixels from the tile's first
           *reinterpret_cast<uint2*>(out0 + step * a.C) =
               make_uint2(pack_e4m3x4(q[0], q[1], q[2], q[3]), pack_e4m3x4(q[4], q[5], q[6], q[7]));
           if (part == 0) {
-            const int64_t row = row0 + step;
+            const int64_t row = rowt + step;
             if (a.expo_out != nullptr) a.expo_out[row * groups + gi] = (int8_t)ex;
             if (a.swizzled != nullptr) {
               const int64_t rt = row & 127;
@@ -273,7 +280,7 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
   // (lane's LDS byte offset of its channel at tile row 8 rh + r4, column 0)
   const int ob8 = (8 * rh + r4) * DWO_ROW8 + 16 * cg + bch;
   const int ob16 = (8 * rh + r4) * DWO_ROW16 + 2 * (16 * cg + bch);
-  uint32_t code[2][8][2];  // 8-bit: [t][cq][0] = 4 codes (columns 4 cq + i); BF16: two packed pairs
+  uint32_t code[2][DW_CQ][2];  // 8-bit: [t][cq][0] = 4 codes (columns 4 cq + i); BF16: two packed pairs
   float oscale = 0.f, oinv8 = 1.f, osc = 1.f, obound = 448.f;
   bool low_clamp = false;
   if (OUT == DW_INT8) {
@@ -291,7 +298,7 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int cq = 0; cq < 8; ++cq) {
+      for (int cq = 0; cq < DW_CQ; ++cq) {
         float v[4] = {acc[t][cq][0], acc[t][cq][1], acc[t][cq][2], acc[t][cq][3]};
         if (ACT == ACT_RELU) {
           if (OUT != DW_INT8) {
@@ -335,7 +342,7 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int cq = 0; cq < 8; ++cq) {
+    for (int cq = 0; cq < DW_CQ; ++cq) {
       if (OUT == DW_BF16) {
         uint8_t* p = sm8 + ob16 + 4 * t * DWO_ROW16 + 4 * cq * (2 * DW_CS);
         *reinterpret_cast<uint16_t*>(p) = (uint16_t)code[t][cq][0];
@@ -360,7 +367,7 @@ __global__ __launch_bounds__(256, 3) void dw5x5_mfma_kernel(const DwArgs a) {
   for (int it = 0; it < DW_TH * DW_TW * CPP / 256; ++it) {
     const int k = tid + 256 * it;
     const int part = k % CPP, px = k / CPP;
-    const int R = px >> 5, X = px & 31;
+    const int R = px / DW_TW, X = px - R * DW_TW;
     const uint4 val = *reinterpret_cast<const uint4*>(sm8 + R * ROWB + X * (DW_CS * ESZ) + 16 * part);
     if (interior || (R < rows && X < cols)) {
       const int64_t row = ((int64_t)b * a.H + y0 + R) * a.W + x0 + X;
