@@ -182,9 +182,10 @@ def _one_kernel_block_wins(value: Tensor) -> bool:
     32 x 8-pixel tiles with all 128 channels on a workgroup (two per CU), so with few tiles each workgroup's four
     channel slices in sequence are the latency, and with many the composite's producer (three workgroups per CU, one
     channel slice each) and pointwise GEMM run faster. Measured on MI355X (256 CUs), MXFP8 / INT8, us, one kernel
-    against composite: 140 tiles 20.7 / 18.0 and 23.2 / 18.9; 200 tiles 22.0 / 23.9 and 24.4 / 26.0; 256 tiles
-    23.5 / 24.7 and 26.3 / 27.6; 456 tiles 29.3 / 42.2 and 31.5 / 40.1; 520 tiles 43.3 / 43.4 and 47.0 / 42.4; 675 tiles
-    44.1 / 42.4 and 49.0 / 44.5; 1300 tiles (2 x 400 x 400) 74.5 / 65.0 and 81.0 / 69.0. Hence the band
+    against composite: 70 tiles 19.7 / 15.5 and 22.5 / 12.8; 140 tiles 20.7 / 15.6 and 23.3 / 16.3; 200 tiles
+    21.8 / 23.2 and 24.3 / 24.9; 256 tiles 23.2 / 23.7 and 25.9 / 26.6; 280 tiles 26.6 / 28.3 and 29.1 / 28.5; 456
+    tiles 29.3 / 40.3 and 31.8 / 36.0; 520 tiles 42.7 / 39.7 and 47.2 / 38.8; 675 tiles 43.9 / 39.9 and 49.1 / 41.4;
+    1300 tiles (2 x 400 x 400) 74.8 / 59.3 and 81.2 / 62.9. Hence the band
     [3/4, 2] x CUs."""
     batch, _, height, width = value.shape
     tiles = batch * -(-height // 8) * -(-width // 32)
