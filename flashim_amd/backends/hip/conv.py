@@ -180,7 +180,7 @@ def _compute_units(index: int) -> int:
 def _one_kernel_block_wins(value: Tensor) -> bool:
     """Whether the one-kernel depthwise-pointwise block beats its two-launch composite at this image: it takes
     32 x 8-pixel tiles with all 128 channels on a workgroup (two per CU), so with few tiles each workgroup's four
-    channel slices in sequence are the latency, and with many the composite's producer (three workgroups per CU, one
+    channel slices in sequence are the latency, and with many the composite's producer (six workgroups per CU, one
     channel slice each) and pointwise GEMM run faster. Measured on MI355X (256 CUs), MXFP8 / INT8, us, one kernel
     against composite: 70 tiles 19.7 / 15.5 and 22.5 / 12.8; 140 tiles 20.7 / 15.6 and 23.3 / 16.3; 200 tiles
     21.8 / 23.2 and 24.3 / 24.9; 256 tiles 23.2 / 23.7 and 25.9 / 26.6; 280 tiles 26.6 / 28.3 and 29.1 / 28.5; 456

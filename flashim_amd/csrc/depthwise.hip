@@ -9,7 +9,7 @@
 //                              (flashim/ops/quantize.py:63-74, 91-100).
 //
 // Layout: input BF16 NHWC [B, H, W, C] (the channels-last memory of [B, C, H, W]); weight BF16 [25, C] (ky, kx major,
-// flashim/quant/passes/separable_conv_block.py:52-55); bias FP32 [C]. Output row = pixel (b, y, x), C channels.
+// flashim/quant/passes/separable_conv_block.py:52-55); bias FP32 or BF16 [C]. Output row = pixel (b, y, x), C channels.
 //
 // Work split: see the tile and matrix-unit comments below (dw5x5_mfma_kernel).
 #include <type_traits>
