@@ -2074,7 +2074,15 @@ __global__ __launch_bounds__(512, 1) void conv_1x1_resident_kernel(const ConvArg
     }
     conv_epilogue<KIND, OUT, 0, MB, NB>(a, acc_i, acc_f, (t / a.n_tiles) * BM + wm * (MB * 16), n0, wn * (NB * 16),
                                         ep_scale, ep_bias, ep_osc);
-    if (next < total) vm_lds_barrier();  // the next tile's activations landed
+    if (next < total) {  // the next tile's activations landed
+      // on the fast epilogue every wavefront issued exactly MB x NB stores (and, with a residual, as many loads) after
+      // the activation loads: waiting for at most that many leaves its stores in flight
+      if (conv_fast_ok<OUT>(a))
+        wait_vm_at_most(MB * NB);
+      else
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+      asm volatile("s_barrier" ::: "memory");
+    }
   }
 }
 
