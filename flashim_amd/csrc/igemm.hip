@@ -1555,8 +1555,8 @@ static int launch_patch(ConvArgs a, hipStream_t stream) {
 }
 
 // ---- Pointwise, register operands --------------------------------------------------------------------------------
-// Pointwise (1 x 1, stride 1) convolutions, a GEMM over pixels, with Cin % 128 == 0, Cin <= 512 and Cout >= 128, where
-// the epilogue (GELU above all) outweighs the MFMAs. Persistent workgroups of 8 wavefronts, one per CU, keep the
+// Pointwise (1 x 1, stride 1) convolutions, a GEMM over pixels, with Cin % 128 == 0, Cin <= 512 or 1024, and Cout >=
+// 128, where the epilogue (GELU above all) or the HBM traffic (big-K contracts) outweighs the MFMAs. Persistent workgroups of 8 wavefronts, one per CU, keep the
 // weights of 128 output channels in LDS (128 x Cin bytes, read-only after the prologue); every wavefront then works
 // alone, with no barrier: it loads its 32 pixel rows of activations straight into MFMA operand registers (the next
 // tile's rows), runs 2 x 8 blocks of 16 x 16 against the LDS weights, and writes
@@ -1570,8 +1570,15 @@ __global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
   constexpr int WTS_BYTES = KS * BN * KC;                // [K step][channel][128 B]
   constexpr int WEXP_BYTES = KIND == KIND_MX ? BN * KS * 4 : 16;
   constexpr int ESZ = OUT == OUT_BF16 ? 2 : 1;
-  constexpr int RB = BN * ESZ, LPP = RB / 16, PPC = 64 / LPP;  // staged row: the 128 channels of one pixel
-  constexpr int SCH = 16 / PPC;                                 // 1 KB stores per 16-pixel round
+  // K steps per operand load phase: a tile's activations for KH steps sit in registers (2 KH x 8 VGPRs), so KS > 4
+  // runs its K loop in phases of 4 steps
+  constexpr int KH = KS < 4 ? KS : 4;
+  static_assert(KS % KH == 0, "whole load phases");
+  // staged row: the 64 channels of one pixel per channel half (HS: KS > 4, where the weights take 128 KB of LDS and a
+  // BF16 half row is still one whole 128-byte line), else all 128
+  constexpr bool HS = KS > 4;
+  constexpr int RB = (HS ? BN / 2 : BN) * ESZ, LPP = RB / 16, PPC = 64 / LPP;
+  constexpr int SCH = 16 / PPC;  // 1 KB stores per 16-pixel round
   static_assert(SCH * PPC == 16, "whole stores per round");
   constexpr int STAGE_BYTES = 8 * 16 * RB;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[WTS_BYTES + STAGE_BYTES + WEXP_BYTES + 3 * BN * 4 + 16];
@@ -1641,7 +1648,7 @@ __global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
   // [64 + 16 g, +16) of the step (rows past M read as zero)
   const __amdgpu_buffer_rsrc_t xr =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.x), (short)0, x_nrec, 0x00020000);
-  auto load_x = [&](int t, v8i (&xa)[MB][KS], int (&sr)[MB][KS]) __attribute__((always_inline)) {
+  auto load_x = [&](int t, int kb, v8i (&xa)[MB][KH], int (&sr)[MB][KH]) __attribute__((always_inline)) {
     const int m0 = (t / a.n_tiles) * (8 * TMW) + wave * TMW;
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
@@ -1649,19 +1656,20 @@ __global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
       if constexpr (XS == 1) {  // the row's E8M0 byte of K block 4 ks + g
         const int r = m < a.M ? m : a.M - 1, rt = r & 127;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const int cb = 4 * ks + g;
-          sr[j][ks] = (int)a.x_swz[(((int64_t)(r >> 7) * a.x_swz_tiles_k + (cb >> 2)) << 9) + (rt & 31) * 16 +
+        for (int k = 0; k < KH; ++k) {
+          const int cb = 4 * (kb + k) + g;
+          sr[j][k] = (int)a.x_swz[(((int64_t)(r >> 7) * a.x_swz_tiles_k + (cb >> 2)) << 9) + (rt & 31) * 16 +
                                    (rt >> 5) * 4 + (cb & 3)];
         }
       }
       const uint32_t base = m < a.M ? (uint32_t)(m * a.Cin + 16 * g) : OOB;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
+      for (int k = 0; k < KH; ++k) {
+        const int ks = kb + k;
         const v4i lo = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)(base + ks * KC), 0, 0));
         const v4i hi =
             __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)(base + ks * KC + 64), 0, 0));
-        xa[j][ks] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        xa[j][k] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
       }
     }
   };
@@ -1706,9 +1714,6 @@ __global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
 
   // one tile: its operand loads are waited for right away; the other wavefront on the SIMD runs meanwhile
   auto run_tile = [&](int t) __attribute__((always_inline)) {
-    v8i xc[MB][KS];
-    int sr[MB][KS];  // per-row scales (XS = 1)
-    load_x(t, xc, sr);
     int wq[NB];  // weight offsets made opaque per tile (else all K steps' weight operands are hoisted)
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
@@ -1724,30 +1729,37 @@ __global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
         acc_i[i][j] = v4i{0, 0, 0, 0};
         acc_f[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
       }
-    v8i wc[2];
-    wc[0] = read_w(wq[0]);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
+    for (int kb = 0; kb < KS; kb += KH) {  // load phases: one for KS <= 4
+      v8i xc[MB][KH];
+      int sr[MB][KH];  // per-row scales (XS = 1)
+      load_x(t, kb, xc, sr);
+      v8i wc[2];
+      wc[0] = read_w(wq[0] + kb * (BN * KC));
 #pragma unroll
-      for (int i = 0; i < NB; ++i) {
-        const int nx = ks * NB + i + 1;  // the next weight block, read while this one's MFMAs run
-        if (nx < KS * NB) wc[nx & 1] = read_w(wq[nx % NB] + (nx / NB) * (BN * KC));
-        const v8i& w = wc[(ks * NB + i) & 1];
+      for (int k = 0; k < KH; ++k)
 #pragma unroll
-        for (int j = 0; j < MB; ++j) {
-          if constexpr (KIND == KIND_INT8) {
-            acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_shufflevector(w, w, 0, 1, 2, 3),
-                                                                __builtin_shufflevector(xc[j][ks], xc[j][ks], 0, 1, 2, 3),
-                                                                acc_i[i][j], 0, 0, 0);
-            acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_shufflevector(w, w, 4, 5, 6, 7),
-                                                                __builtin_shufflevector(xc[j][ks], xc[j][ks], 4, 5, 6, 7),
-                                                                acc_i[i][j], 0, 0, 0);
-          } else {
-            acc_f[i][j] = mfma_scale_opsel(w, xc[j][ks], acc_f[i][j], i & 3, swp[ks][i >> 2],
-                                           XS == 1 ? sr[j][ks] : sxs[ks]);
+        for (int i = 0; i < NB; ++i) {
+          const int ks = kb + k;
+          const int nx = k * NB + i + 1;  // the next weight block of this phase, read while this one's MFMAs run
+          if (nx < KH * NB) wc[nx & 1] = read_w(wq[nx % NB] + (kb + nx / NB) * (BN * KC));
+          const v8i& w = wc[(k * NB + i) & 1];
+#pragma unroll
+          for (int j = 0; j < MB; ++j) {
+            if constexpr (KIND == KIND_INT8) {
+              acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_shufflevector(w, w, 0, 1, 2, 3),
+                                                                  __builtin_shufflevector(xc[j][k], xc[j][k], 0, 1, 2, 3),
+                                                                  acc_i[i][j], 0, 0, 0);
+              acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_shufflevector(w, w, 4, 5, 6, 7),
+                                                                  __builtin_shufflevector(xc[j][k], xc[j][k], 4, 5, 6, 7),
+                                                                  acc_i[i][j], 0, 0, 0);
+            } else {
+              acc_f[i][j] = mfma_scale_opsel(w, xc[j][k], acc_f[i][j], i & 3, swp[ks][i >> 2],
+                                             XS == 1 ? sr[j][k] : sxs[ks]);
+            }
           }
         }
-      }
+    }
     // the accumulators pinned (else the MFMAs are sunk into the epilogue with their operands live)
 #pragma unroll
     for (int i = 0; i < NB; ++i)
@@ -1761,7 +1773,22 @@ __global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
     // epilogue: 16 pixels per round, staged in this wavefront's LDS area and written in whole lines
     const int m0 = (t / a.n_tiles) * (8 * TMW) + wave * TMW;
     const int sl = lane % LPP;
-    const bool cvalid = n0 + sl * (16 / ESZ) < a.Cout;
+    // the staged rows out in whole lines: 16 pixels x RB bytes, from channel n0 + nh on
+    auto write_stage = [&](int r, int nh) __attribute__((always_inline)) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
+      const bool cvalid = n0 + nh + sl * (16 / ESZ) < a.Cout;
+#pragma unroll
+      for (int c = 0; c < SCH; ++c) {
+        const int pl = c * PPC + lane / LPP;
+        typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 v = *reinterpret_cast<const u32x4*>(my_stage + pl * RB + ((sl ^ stage_swz(pl)) & (LPP - 1)) * 16);
+        const int mm = m0 + r * 16 + pl;
+        const uint32_t off =
+            cvalid && mm < a.M ? ((uint32_t)mm * (uint32_t)a.out_ld + (uint32_t)(n0 + nh)) * ESZ + sl * 16 : OOB;
+        __builtin_amdgcn_raw_buffer_store_b128(v, orsrc, (int)off, 0, 0);
+      }
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
+    };
     with_epilogue_variant(a, [&](auto gv, auto rv) __attribute__((always_inline)) {
       constexpr int G = decltype(gv)::value;
       constexpr bool R = decltype(rv)::value;
@@ -1783,21 +1810,14 @@ __global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
             ai[i][0] = acc_i[4 * h + i][r];
             af[i][0] = acc_f[4 * h + i][r];
           }
-          conv_epilogue_fast<KIND, OUT, 1, 4, G, R, RB>(a, ai, af, mrow, n0, 64 * h, ch, my_stage, spix);
+          if constexpr (HS) {  // this half's 64 channels staged as a row of their own, then written out
+            conv_epilogue_fast<KIND, OUT, 1, 4, G, R, RB>(a, ai, af, mrow, n0 + 64 * h, 0, ch, my_stage, spix);
+            write_stage(r, 64 * h);
+          } else {
+            conv_epilogue_fast<KIND, OUT, 1, 4, G, R, RB>(a, ai, af, mrow, n0, 64 * h, ch, my_stage, spix);
+          }
         }
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
-#pragma unroll
-        for (int c = 0; c < SCH; ++c) {
-          const int pl = c * PPC + lane / LPP;
-          typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-          const u32x4 v =
-              *reinterpret_cast<const u32x4*>(my_stage + pl * RB + ((sl ^ stage_swz(pl)) & (LPP - 1)) * 16);
-          const int mm = m0 + r * 16 + pl;
-          const uint32_t off =
-              cvalid && mm < a.M ? ((uint32_t)mm * (uint32_t)a.out_ld + (uint32_t)n0) * ESZ + sl * 16 : OOB;
-          __builtin_amdgcn_raw_buffer_store_b128(v, orsrc, (int)off, 0, 0);
-        }
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
+        if constexpr (!HS) write_stage(r, 0);
       }
     });
   };
@@ -1805,12 +1825,13 @@ __global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
   for (int t = first; t < total; t += stride) run_tile(t);
 }
 
-// Whether the pointwise kernel applies: 1 x 1, stride 1, no padding, 128 <= Cin <= 512 with Cin % 128 == 0,
+// Whether the pointwise kernel applies: 1 x 1, stride 1, no padding, Cin one of 128, 256, 384, 512 or 1024,
 // Cout >= 128 (Cout % 16 == 0 by the fast epilogue), dense 16-byte aligned output, no pooling / per-row scales.
 static int pw_ks(const ConvArgs& a, int lw, bool fast_ok) {
   if (lw != 16 || !fast_ok || a.pool_out != nullptr || a.a_scale_rows != nullptr) return 0;
   if (a.kh != 1 || a.kw != 1 || a.sh != 1 || a.sw != 1 || a.ph != 0 || a.pw != 0) return 0;
-  if (a.Cin % KC != 0 || a.Cin > 4 * KC || a.Cout < 128 || ((uintptr_t)a.out & 15) != 0 || a.out_ld != a.Cout)
+  if (a.Cin % KC != 0 || (a.Cin > 4 * KC && a.Cin != 8 * KC) || a.Cout < 128 || ((uintptr_t)a.out & 15) != 0 ||
+      a.out_ld != a.Cout)
     return 0;
   if ((int64_t)a.M * a.Cin >= (1LL << 31) - 16 || (int64_t)a.Cout * a.Cin >= (1LL << 31)) return 0;
   // at least two 256-pixel tiles per CU: with fewer, most wavefronts run one tile with nothing to overlap its loads
@@ -1826,7 +1847,8 @@ static void launch_pw_ks(const ConvArgs& a, int ks, dim3 grid, hipStream_t strea
     case 1: conv_pw_kernel<KIND, OUT, 1, XS><<<grid, dim3(512), 0, stream>>>(a); break;
     case 2: conv_pw_kernel<KIND, OUT, 2, XS><<<grid, dim3(512), 0, stream>>>(a); break;
     case 3: conv_pw_kernel<KIND, OUT, 3, XS><<<grid, dim3(512), 0, stream>>>(a); break;
-    default: conv_pw_kernel<KIND, OUT, 4, XS><<<grid, dim3(512), 0, stream>>>(a); break;
+    case 4: conv_pw_kernel<KIND, OUT, 4, XS><<<grid, dim3(512), 0, stream>>>(a); break;
+    default: conv_pw_kernel<KIND, OUT, 8, XS><<<grid, dim3(512), 0, stream>>>(a); break;
   }
 }
 

@@ -503,10 +503,11 @@ def test_mxfp8_conv2d_patch_tiles(case):
                            .view(torch.uint8)), name
 
 
-# (name, image (B, H, W), Cin, Cout): pointwise shapes (1 x 1, stride 1, Cin a multiple of 128 up to 512, Cout >= 128):
-# 1 to 4 K steps, a partial last tile of pixels, a partial channel block; the large ones run the register-operand
-# pointwise kernel, the "resident" ones (one to two 160-pixel tiles per CU on 256 CUs) the whole-K kernel, the small
-# ones the one-round kernels
+# (name, image (B, H, W), Cin, Cout): pointwise shapes (1 x 1, stride 1, Cin a multiple of 128 up to 512 or 1024,
+# Cout >= 128): 1 to 4 and 8 K steps, a partial last tile of pixels, a partial channel block; the large ones run the
+# register-operand pointwise kernel (at 8 K steps in two load phases, its output staged in 64-channel half rows), the
+# "resident" ones (one to two 160-pixel tiles per CU on 256 CUs) the whole-K kernel, the small ones the one-round
+# kernels
 ROW_CASES = [
     ("k1_n128_resident", (2, 150, 151), 128, 128),
     ("k2_n144_resident", (2, 110, 111), 256, 144),
@@ -521,6 +522,10 @@ ROW_CASES = [
     ("k2_n144_big", (1, 256, 257), 256, 144),
     ("k3_n256_big", (2, 160, 210), 384, 256),
     ("k4_n512_big", (2, 128, 129), 512, 512),
+    # the refiner stack's s = 4 contract (1024 -> 256), and a partial channel block at 8 K steps
+    ("k8_n256_big", (2, 200, 200), 1024, 256),
+    ("k8_n144_big", (1, 256, 257), 1024, 144),
+    ("k8_n256", (1, 30, 31), 1024, 256),
 ]
 PW_GEO = (1, 1, 1, 1, 0, 0, 1, 1)
 

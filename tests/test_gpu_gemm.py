@@ -107,10 +107,11 @@ def test_mxfp8_linear(rows, k, n, has_bias):
     _assert_mx_close(got, want)
 
 
-# the last three have at least two 256-row tiles per CU (256 CUs) and run the register-operand pointwise kernel with
-# per-row swizzled scales; the others the one-round kernels
+# the last four have at least two 256-row tiles per CU (256 CUs) and run the register-operand pointwise kernel with
+# per-row swizzled scales (K = 1024: two load phases of 4 K steps, a partial last tile); the others the one-round
+# kernels
 @pytest.mark.parametrize("m,k,n", [(1, 32, 32), (300, 256, 96), (4096, 128, 128), (1000, 512, 320),
-                                   (140000, 128, 128), (70000, 256, 256), (40001, 512, 512)])
+                                   (140000, 128, 128), (70000, 256, 256), (40001, 512, 512), (65600, 1024, 256)])
 @pytest.mark.parametrize("has_bias", [False, True])
 def test_mxfp8_scaled_mm(m, k, n, has_bias):
     g = torch.Generator().manual_seed(m + n)
