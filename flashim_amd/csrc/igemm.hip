@@ -953,8 +953,22 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
   }
 
   int ld_ky = 0, ld_kx = 0, ld_c0 = 0;
-  // issue the loads of the next (tap, channel chunk) step into LDS stage `buf`; its raw MX exponent bytes into (sx, sw)
-  auto issue = [&](uint8_t* st, int& sx, int (&sw)[NB], bool& ok) __attribute__((always_inline)) {
+  // the raw MX exponent bytes of the next (tap, channel chunk) step into (sx, sw). Loaded on every step, also past the
+  // last (then from step 0's address, unused): a load issued only on some paths leaves its register a join of two
+  // values, and the copy at the join waits for the load (a full vmcnt wait that drains the operand prefetch)
+  auto load_exponents = [&](bool more, int& sx, int (&sw)[NB], bool& ok) __attribute__((always_inline)) {
+    if (KIND == KIND_MX) {
+      const int blk = (ld_c0 >> 5) + g;
+      const int cblk = blk < cblocks ? blk : cblocks - 1;
+      sx = (int)a.x_expo[more ? cblk : 0];
+      ok = blk < cblocks;
+      const int wblk = more ? (ld_ky * a.kw + ld_kx) * cblocks + cblk : 0;
+#pragma unroll
+      for (int i = 0; i < NB; ++i) sw[i] = (int)wexp_row[i][wblk];
+    }
+  };
+  // issue the loads of the next (tap, channel chunk) step into LDS stage `st` and move to the step after it
+  auto issue = [&](uint8_t* st) __attribute__((always_inline)) {
     const int dy = ld_ky * a.dh, dx = ld_kx * a.dw;
     const int xdelta = (dy * a.W + dx) * a.Cin + ld_c0;
     const int wdelta = (ld_ky * a.kw + ld_kx) * a.Cin + ld_c0;
@@ -978,15 +992,6 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
               __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), (short)0, w_nrec, 0x00020000),
               (lds_void_t*)(st + c * 1024), 16, off, 0, 0, 0);
       }
-    }
-    if (KIND == KIND_MX) {
-      const int blk = (ld_c0 >> 5) + g;
-      const int cblk = blk < cblocks ? blk : cblocks - 1;
-      sx = (int)a.x_expo[cblk];
-      ok = blk < cblocks;
-      const int wblk = (ld_ky * a.kw + ld_kx) * cblocks + cblk;
-#pragma unroll
-      for (int i = 0; i < NB; ++i) sw[i] = (int)wexp_row[i][wblk];
     }
     ld_c0 += KC;
     if (ld_c0 >= a.Cin) {
@@ -1020,7 +1025,7 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
   }
 
   // one K step from stage `cur` (exponent set ec); the loads of step kt + NST - 1 go into stage `nxt` (set en)
-  auto step = [&](int kt, const uint8_t* cur, uint8_t* nxt, int ec, int en) __attribute__((always_inline)) {
+  auto step_live = [&](int kt, const uint8_t* cur, uint8_t* nxt, int ec, int en) __attribute__((always_inline)) {
     // this step's fragments first: the next loads into LDS are issued after them, so no read waits on those. MXFP8
     // operands are built as the 8-register tuples the MFMA reads, straight from their two LDS reads (built later,
     // each tuple costs four 64-bit register moves per step)
@@ -1050,13 +1055,20 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
     }
     int sxs = 127, sw[NB];
     if (KIND == KIND_MX) {
+      // the raw bytes made opaque here, where they are used: otherwise the scale arithmetic is moved up to the loads
+      // (two steps earlier), which then wait for their data on the spot
+      asm volatile("" : "+v"(esx[ec]));
+#pragma unroll
+      for (int i = 0; i < NB; ++i) asm volatile("" : "+v"(esw[ec][i]));
       sxs = eok[ec] ? esx[ec] + 127 : 127;
 #pragma unroll
       for (int i = 0; i < NB; ++i) sw[i] = eok[ec] ? w_scale_byte(a, esw[ec][i]) : 127;
     }
     const bool more = kt + NST - 1 < nk;
     __builtin_amdgcn_sched_barrier(0);
-    if (more) issue(nxt, esx[en], esw[en], eok[en]);
+    load_exponents(more, esx[en], esw[en], eok[en]);  // before the stage loads: the wait below then spares those
+    __builtin_amdgcn_sched_barrier(0);
+    if (more) issue(nxt);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (KIND == KIND_INT8) {
 #pragma unroll
@@ -1074,33 +1086,45 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_wide_kernel(const ConvArgs 
           acc_f[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[i], xf[j], acc_f[i][j], 0, 0, 0, sw[i], 0, sxs);
     }
     __builtin_amdgcn_sched_barrier(0);  // the wait for the next stage stays behind this step's MFMAs
-    // step kt + 1's loads were issued one step earlier (or in the prologue); when this step issued loads, at least
-    // CPW_MIN of this wavefront's loads are younger than all of them, so vmcnt <= CPW_MIN means they have landed
+    // step kt + 1's stage loads were issued one step earlier (or in the prologue); when this step issued loads, at
+    // least CPW_MIN of this wavefront's loads (its stage loads) are younger than all of them, so vmcnt <= CPW_MIN means
+    // they have landed (it may also wait for this step's exponent bytes, issued first, a whole MFMA phase earlier)
     if (NST == 3 && more)
       asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(CPW_MIN) : "memory");
     else
       vm_lds_barrier();
   };
+  // a step of the unconditional stage rotation: past the last step (kt >= nk: a uniform branch) only the exponent
+  // registers are loaded, so that no loaded register is a join of a load with an older value
+  auto step = [&](int kt, const uint8_t* cur, uint8_t* nxt, int ec, int en) __attribute__((always_inline)) {
+    if (kt < nk)
+      step_live(kt, cur, nxt, ec, en);
+    else
+      load_exponents(false, esx[en], esw[en], eok[en]);
+  };
 
   if constexpr (NST == 3) {
-    issue(st0, esx[0], esw[0], eok[0]);
+    load_exponents(true, esx[0], esw[0], eok[0]);
+    issue(st0);
     if (nk > 1) {
-      issue(st1, esx[1], esw[1], eok[1]);
+      load_exponents(true, esx[1], esw[1], eok[1]);
+      issue(st1);
       asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(CPW_MIN) : "memory");
     } else {
       vm_lds_barrier();
     }
     for (int kt = 0; kt < nk; kt += 3) {
       step(kt, st0, st2, 0, 2);
-      if (kt + 1 < nk) step(kt + 1, st1, st0, 1, 0);
-      if (kt + 2 < nk) step(kt + 2, st2, st1, 2, 1);
+      step(kt + 1, st1, st0, 1, 0);
+      step(kt + 2, st2, st1, 2, 1);
     }
   } else {
-    issue(st0, esx[0], esw[0], eok[0]);
+    load_exponents(true, esx[0], esw[0], eok[0]);
+    issue(st0);
     vm_lds_barrier();
     for (int kt = 0; kt < nk; kt += 2) {
       step(kt, st0, st1, 0, 1);
-      if (kt + 1 < nk) step(kt + 1, st1, st0, 1, 0);
+      step(kt + 1, st1, st0, 1, 0);
     }
   }
 
@@ -1568,6 +1592,7 @@ template <int KIND, int OUT, int KS, int XS = 0>
 __global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
   constexpr int BN = 128, MB = 2, NB = 8, TMW = MB * 16;  // a wavefront's tile: 32 pixels x 128 channels
   constexpr int WTS_BYTES = KS * BN * KC;                // [K step][channel][128 B]
+  constexpr int XEXP_BYTES = (KS * 4 + 15) / 16 * 16;    // the activations' MX exponent bytes (XS = 0)
   constexpr int WEXP_BYTES = KIND == KIND_MX ? BN * KS * 4 : 16;
   constexpr int ESZ = OUT == OUT_BF16 ? 2 : 1;
   // K steps per operand load phase: a tile's activations for KH steps sit in registers (2 KH x 8 VGPRs), so KS > 4
@@ -1581,7 +1606,7 @@ __global__ __launch_bounds__(512, 1) void conv_pw_kernel(const ConvArgs a) {
   constexpr int SCH = 16 / PPC;  // 1 KB stores per 16-pixel round
   static_assert(SCH * PPC == 16, "whole stores per round");
   constexpr int STAGE_BYTES = 8 * 16 * RB;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[WTS_BYTES + STAGE_BYTES + WEXP_BYTES + 3 * BN * 4 + 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[WTS_BYTES + STAGE_BYTES + WEXP_BYTES + 3 * BN * 4 + XEXP_BYTES];
   uint8_t* const wts = smem;
   uint8_t* const stage = wts + WTS_BYTES;
   uint8_t* const wexp_s = stage + STAGE_BYTES;           // [channel][K block] (MXFP8)
