@@ -166,15 +166,8 @@ __device__ __forceinline__ EpiChannels<NB> epi_channels(int nl0, const float* ep
 // pixel, 16-byte slot s of row p at slot s ^ stage_swz(p) (the caller writes the tile out in whole lines).
 __device__ __forceinline__ int stage_swz(int p) { return (p >> 1) & 7; }
 
-// Cache policy of the epilogue's global stores (the buffer store's aux operand): 0 writes back from L2 (the default:
-// the next kernel reads the output from L2); CPOL_WRITE_THROUGH (sc0 sc1, system scope) writes through to memory
-// during the kernel, so the end-of-kernel release has no dirty output lines left to write back. The L2 of one XCD is
-// not coherent with the others, so that write-back is otherwise serialized after the last workgroup.
-constexpr int CPOL_WRITE_THROUGH = 1 | 16;
-
 // GELU: 0 none (ReLU or the identity as one IEEE maximum), 1 GELU without ReLU (no maximum), 2 ReLU then GELU.
-// CPOL: the stores' cache policy (above).
-template <int KIND, int OUT, int MB, int NB, int GELU, bool RES = false, int STAGE_RB = 0, int CPOL = 0>
+template <int KIND, int OUT, int MB, int NB, int GELU, bool RES = false, int STAGE_RB = 0>
 __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
                                                    const v4f (&acc_f)[NB][MB], const int (&mrow)[MB], int n_tile0,
                                                    int nl0, const EpiChannels<NB>& ch, uint8_t* stage = nullptr,
@@ -282,7 +275,7 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
         if constexpr (STAGE_RB > 0)
           *reinterpret_cast<u32x2*>(sd) = u32x2{lo, hi};
         else
-          __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rsrc, (int)off, 0, CPOL);
+          __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rsrc, (int)off, 0, 0);
       } else {
         uint32_t pk;
         if (OUT == OUT_INT8) {  // the block's 4 values share one near-tie test (one wave-uniform branch)
@@ -297,7 +290,7 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
         if constexpr (STAGE_RB > 0)
           *reinterpret_cast<uint32_t*>(sd) = pk;
         else
-          __builtin_amdgcn_raw_buffer_store_b32(pk, rsrc, (int)off, 0, CPOL);
+          __builtin_amdgcn_raw_buffer_store_b32(pk, rsrc, (int)off, 0, 0);
       }
     }
     // this row block's stores (all NB x 16 channels of 16 pixels: whole 128-byte lines of a BF16 output) go out before
@@ -309,13 +302,13 @@ __device__ __forceinline__ void conv_epilogue_fast(const ConvArgs& a, const v4i 
 // The fast epilogue's variants (GELU with or without a ReLU before it, dense residual) for lane rows mrow, into global
 // memory (STAGE_RB = 0) or an LDS staging tile (see conv_epilogue_fast's STAGE_RB); the caller has checked
 // conv_fast_ok.
-template <int KIND, int OUT, int MB, int NB, int STAGE_RB = 0, int CPOL = 0>
+template <int KIND, int OUT, int MB, int NB, int STAGE_RB = 0>
 __device__ __forceinline__ void conv_epilogue_any(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
                                                   const v4f (&acc_f)[NB][MB], const int (&mrow)[MB], int n_tile0,
                                                   int nl0, const EpiChannels<NB>& ch, uint8_t* stage = nullptr,
                                                   const int* spix = nullptr) {
 #define FIM_EPI(G, R) \
-  conv_epilogue_fast<KIND, OUT, MB, NB, G, R, STAGE_RB, CPOL>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch, stage, spix)
+  conv_epilogue_fast<KIND, OUT, MB, NB, G, R, STAGE_RB>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch, stage, spix)
   const int act = a.gelu ? (a.relu_pre ? 2 : 1) : 0;
   if (a.residual != nullptr) {
     if (act == 1) FIM_EPI(1, true);
@@ -352,19 +345,19 @@ __device__ __forceinline__ void with_epilogue_variant(const ConvArgs& a, F&& f) 
   }
 }
 
-template <int KIND, int OUT, int MB, int NB, int CPOL = 0>
+template <int KIND, int OUT, int MB, int NB>
 __device__ __forceinline__ void conv_epilogue_rows(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
                                                    const v4f (&acc_f)[NB][MB], const int (&mrow)[MB], int n_tile0,
                                                    int nl0, const EpiChannels<NB>& ch) {
-  conv_epilogue_any<KIND, OUT, MB, NB, 0, CPOL>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch);
+  conv_epilogue_any<KIND, OUT, MB, NB>(a, acc_i, acc_f, mrow, n_tile0, nl0, ch);
 }
 
-template <int KIND, int OUT, int MB, int NB, int CPOL = 0>
+template <int KIND, int OUT, int MB, int NB>
 __device__ __forceinline__ void conv_epilogue_rows(const ConvArgs& a, const v4i (&acc_i)[NB][MB],
                                                    const v4f (&acc_f)[NB][MB], const int (&mrow)[MB], int n_tile0,
                                                    int nl0, const float* ep_scale, const float* ep_bias,
                                                    const float* ep_osc) {
-  conv_epilogue_rows<KIND, OUT, MB, NB, CPOL>(a, acc_i, acc_f, mrow, n_tile0, nl0,
+  conv_epilogue_rows<KIND, OUT, MB, NB>(a, acc_i, acc_f, mrow, n_tile0, nl0,
                                         epi_channels<NB>(nl0, ep_scale, ep_bias, ep_osc));
 }
 
@@ -380,7 +373,7 @@ __host__ __device__ __forceinline__ bool conv_fast_ok(const ConvArgs& a) {
          (int64_t)a.M * a.out_ld * (OUT == OUT_BF16 ? 2 : 1) < (int64_t)0x7fffffff;
 }
 
-template <int KIND, int OUT, int POOL, int MB, int NB, int CPOL = 0>
+template <int KIND, int OUT, int POOL, int MB, int NB>
 __device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc_i)[NB][MB], const v4f (&acc_f)[NB][MB],
                                               int row0, int n_tile0, int nl0, const float* ep_scale,
                                               const float* ep_bias, const float* ep_osc) {
@@ -388,7 +381,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs& a, const v4i (&acc
     int mrow[MB];
 #pragma unroll
     for (int j = 0; j < MB; ++j) mrow[j] = row0 + j * 16 + (threadIdx.x & 15);
-    conv_epilogue_rows<KIND, OUT, MB, NB, CPOL>(a, acc_i, acc_f, mrow, n_tile0, nl0, ep_scale, ep_bias, ep_osc);
+    conv_epilogue_rows<KIND, OUT, MB, NB>(a, acc_i, acc_f, mrow, n_tile0, nl0, ep_scale, ep_bias, ep_osc);
     return;
   }
   const int lane = threadIdx.x & 63;
@@ -2126,8 +2119,8 @@ __global__ __launch_bounds__(512, 1) void conv_1x1_resident_kernel(const ConvArg
 #pragma unroll
       for (int st = 0; st < KS; ++st) load_a_step(next, st);
     }
-    conv_epilogue<KIND, OUT, 0, MB, NB, CPOL_WRITE_THROUGH>(a, acc_i, acc_f, (t / a.n_tiles) * BM + wm * (MB * 16), n0,
-                                                            wn * (NB * 16), ep_scale, ep_bias, ep_osc);
+    conv_epilogue<KIND, OUT, 0, MB, NB>(a, acc_i, acc_f, (t / a.n_tiles) * BM + wm * (MB * 16), n0, wn * (NB * 16),
+                                        ep_scale, ep_bias, ep_osc);
     if (next < total) {  // the next tile's activations landed
       // on the fast epilogue every wavefront issued exactly MB x NB stores (and, with a residual, as many loads) after
       // the activation loads: waiting for at most that many leaves its stores in flight
