@@ -1573,11 +1573,11 @@ static int launch_patch(ConvArgs a, hipStream_t stream) {
 
 // ---- Pointwise, register operands --------------------------------------------------------------------------------
 // Pointwise (1 x 1, stride 1) convolutions, a GEMM over pixels, with Cin % 128 == 0, Cin <= 512 or 1024, and Cout >=
-// 128, where the epilogue (GELU above all) or the HBM traffic (big-K contracts) outweighs the MFMAs. Persistent workgroups of 8 wavefronts, one per CU, keep the
-// weights of 128 output channels in LDS (128 x Cin bytes, read-only after the prologue); every wavefront then works
-// alone, with no barrier: it loads its 32 pixel rows of activations straight into MFMA operand registers (the next
-// tile's rows), runs 2 x 8 blocks of 16 x 16 against the LDS weights, and writes
-// its epilogue through a private LDS staging area in whole lines. Two wavefronts per SIMD drift apart, so one's loads
+// 128, where the epilogue (GELU above all) or the HBM traffic (big-K contracts) outweighs the MFMAs. Persistent
+// workgroups of 8 wavefronts, one per CU, keep the weights of 128 output channels in LDS (128 x Cin bytes, read-only
+// after the prologue); every wavefront then works alone, with no barrier: it loads its tile's 32 pixel rows of
+// activations straight into MFMA operand registers (up to 4 K steps at a time), runs 2 x 8 blocks of 16 x 16 against
+// the LDS weights, and writes its epilogue through a private LDS staging area in whole lines. Two wavefronts per SIMD drift apart, so one's loads
 // and MFMAs run while the other's epilogue keeps the VALU busy.
 // XS = 1: MXFP8 activations with per-row E8M0 scales in the 128x4 swizzled layout (mxfp8_scaled_mm's dynamic
 // quantization), read per tile with the rows; XS = 0: per-channel-block exponents.
