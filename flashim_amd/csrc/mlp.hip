@@ -117,9 +117,17 @@ __global__ __launch_bounds__(256, (mlp_wgs_per_cu<KIND, SEM>())) void refiner_ml
   const int8_t* hexp = static_cast<const int8_t*>(a.h_scale);
   // MX: the scales 2^e of this wave's two 32-channel hidden blocks (2 wave, 2 wave + 1)
   float hsc_w[2] = {1.0f, 1.0f};
+  // MX: the contract's activation scales (E8M0) of the lane's K blocks 4 s + g, read once here: read in the tile loop
+  // (the output stores may alias them, so the compiler reloads them per tile), their wait also drained the next tile's
+  // prefetch
+  int hsx[MLP_H / 128];
+#pragma unroll
+  for (int s = 0; s < MLP_H / 128; ++s) hsx[s] = 127;
   if (KIND == MLP_MX) {
     hsc_w[0] = exp2_int((int)hexp[2 * __builtin_amdgcn_readfirstlane(wave)]);
     hsc_w[1] = exp2_int((int)hexp[2 * __builtin_amdgcn_readfirstlane(wave) + 1]);
+#pragma unroll
+    for (int s = 0; s < MLP_H / 128; ++s) hsx[s] = (int)hexp[4 * s + g] + 127;
   }
 
   // per-lane pieces of the tile loop
@@ -142,6 +150,13 @@ __global__ __launch_bounds__(256, (mlp_wgs_per_cu<KIND, SEM>())) void refiner_ml
       r[i] = v;
     }
   };
+  // the output as a buffer (P x C BF16 < 2 GiB: checked by the host), its descriptor from uniform operands
+  const uint64_t out_addr = (uint64_t)a.out;
+  const uint64_t out_u = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(out_addr >> 32)) << 32) |
+                         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)out_addr);
+  const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<void*>(out_u), (short)0, __builtin_amdgcn_readfirstlane((int)((uint32_t)a.P * MLP_C * 2u)),
+      0x00020000);
   uint4 cur = load_tile(blockIdx.x);
   uint2 res_cur[4], res_nxt[4];
   load_res(blockIdx.x, res_cur);
@@ -364,7 +379,7 @@ __global__ __launch_bounds__(256, (mlp_wgs_per_cu<KIND, SEM>())) void refiner_ml
           const v4i hl = *reinterpret_cast<const v4i*>(&hs[prow * MLP_H + ((sl ^ (prow & 15)) << 4)]);
           const v4i hh = *reinterpret_cast<const v4i*>(&hs[prow * MLP_H + ((sh ^ (prow & 15)) << 4)]);
           const v8i hf = v8i{hl[0], hl[1], hl[2], hl[3], hh[0], hh[1], hh[2], hh[3]};
-          const int sx = (int)hexp[4 * s + g] + 127;  // lane group g scales K block 4 s + g
+          const int sx = hsx[s];  // lane group g scales K block 4 s + g
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int c = 16 * i + r16;
@@ -393,9 +408,12 @@ __global__ __launch_bounds__(256, (mlp_wgs_per_cu<KIND, SEM>())) void refiner_ml
           y[2] = __fadd_rn(y[2], u2f(res[i].y << 16));
           y[3] = __fadd_rn(y[3], u2f(res[i].y & 0xffff0000u));
         }
-        if (pok)
-          *reinterpret_cast<uint2*>(a.out + (int64_t)px * MLP_C + c0) =
-              make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+        // an unconditional buffer store (pixels past P at an offset past the buffer's end): the compiler then counts
+        // the stores exactly, and the next tile's wait for its prefetched input does not wait for them
+        typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+        const uint32_t off = pok ? (uint32_t)(px * MLP_C + c0) * 2u : 0x80000000u;
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])}, orsrc, (int)off, 0,
+                                              0);
       }
     }
 #pragma unroll
