@@ -2056,7 +2056,12 @@ __global__ __launch_bounds__(512, 1) void conv_1x1_resident_kernel(const ConvArg
     fr_w[i] = r * KC + ((g ^ ((r >> 1) & 7)) << 4);
   }
 
-  for (int t = first; t < total; t += stride) {
+  // one tile; FIRST (a constant): the first tile, whose K steps wait for their own loads. The first tile is peeled off
+  // the loop so that the loop's K steps follow only the counted wait at the end of the previous tile: with the first
+  // tile's waits under a branch inside the loop, the compiler's own wait before the LDS reads merged both paths and
+  // became a full vmcnt(0), which also waited for the previous tile's output stores
+  auto run_tile = [&](int t, auto first_c) __attribute__((always_inline)) {
+    constexpr bool FIRST = decltype(first_c)::value;
     v4i acc_i[NB][MB];
     v4f acc_f[NB][MB];
 #pragma unroll
@@ -2068,7 +2073,7 @@ __global__ __launch_bounds__(512, 1) void conv_1x1_resident_kernel(const ConvArg
       }
 #pragma unroll
     for (int st = 0; st < KS; ++st) {
-      if (t == first) {  // step st of the first tile (and, at step 0, the staged epilogue operands) landed everywhere
+      if constexpr (FIRST) {  // step st of the first tile (and, at step 0, the staged epilogue operands) landed
         wait_vm_at_most((KS - 1 - st) * PER_STEP);
         asm volatile("s_barrier" ::: "memory");
       }
@@ -2119,24 +2124,29 @@ __global__ __launch_bounds__(512, 1) void conv_1x1_resident_kernel(const ConvArg
 #pragma unroll
       for (int st = 0; st < KS; ++st) load_a_step(next, st);
     }
-    conv_epilogue<KIND, OUT, 0, MB, NB>(a, acc_i, acc_f, (t / a.n_tiles) * BM + wm * (MB * 16), n0, wn * (NB * 16),
-                                        ep_scale, ep_bias, ep_osc);
-    if (next < total) {  // the next tile's activations landed
-      // on the fast epilogue every wavefront issued exactly MB x NB stores (and, with a residual, as many loads) after
-      // the activation loads: waiting for at most that many leaves its stores in flight
-      if (conv_fast_ok<OUT>(a))
-        wait_vm_at_most(MB * NB);
-      else
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
-      asm volatile("s_barrier" ::: "memory");
+    {  // the fast epilogue (the host launches this kernel only where it applies)
+      int mrow[MB];
+#pragma unroll
+      for (int j = 0; j < MB; ++j) mrow[j] = (t / a.n_tiles) * BM + wm * (MB * 16) + j * 16 + (lane & 15);
+      conv_epilogue_rows<KIND, OUT, MB, NB>(a, acc_i, acc_f, mrow, n0, wn * (NB * 16), ep_scale, ep_bias, ep_osc);
     }
-  }
+    // the next tile's activations landed: every wavefront issued exactly MB x NB stores (and, with a residual, as
+    // many loads) after the activation loads, so waiting for at most that many leaves its stores in flight. Also after
+    // the last tile (nothing to wait for then but the stores): unconditional, so that the compiler's own accounting
+    // sees this wait on every path into the next tile's LDS reads
+    wait_vm_at_most(MB * NB);
+    asm volatile("s_barrier" ::: "memory");
+  };
+  run_tile(first, std::true_type{});
+  for (int t = first + stride; t < total; t += stride) run_tile(t, std::false_type{});
 }
 
 // Whether the resident-K pointwise kernel applies: the pointwise kernel's shape conditions (1 x 1, stride 1, no
-// padding, Cin % 128 == 0 up to 512, 16-byte aligned operands and output) and at least one 160-pixel tile per CU.
-static int res_ks(const ConvArgs& a, int lw) {
-  if (lw != 16 || a.pool_out != nullptr || a.a_scale_rows != nullptr || a.x_swz != nullptr) return 0;
+// padding, Cin % 128 == 0 up to 512, 16-byte aligned operands and output), the fast epilogue and at least one
+// 160-pixel tile per CU.
+static int res_ks(const ConvArgs& a, int lw, bool fast_ok) {
+  // the fast epilogue only: the kernel's waits count its stores (the general epilogue's shapes take the other kernels)
+  if (lw != 16 || !fast_ok || a.pool_out != nullptr || a.a_scale_rows != nullptr || a.x_swz != nullptr) return 0;
   if (a.kh != 1 || a.kw != 1 || a.sh != 1 || a.sw != 1 || a.ph != 0 || a.pw != 0) return 0;
   if (a.Cin % KC != 0 || a.Cin > 4 * KC || a.Cout < 128) return 0;
   if ((int64_t)a.M * a.Cin >= (1LL << 31) - 16 || (int64_t)a.Cout * a.Cin >= (1LL << 31)) return 0;
@@ -2397,7 +2407,7 @@ static int launch_conv(ConvArgs a, hipStream_t stream) {
   const bool fast_ok = a.out_mode == OUT_BF16 ? conv_fast_ok<OUT_BF16>(a) : conv_fast_ok<OUT_INT8>(a);
   if (patch_ok(a, lw, fast_ok)) return launch_patch<KIND>(a, stream);
   if (const int ks = pw_ks(a, lw, fast_ok)) return launch_pw<KIND>(a, ks, stream);
-  if (const int ks = res_ks(a, lw)) return launch_res<KIND>(a, ks, stream);
+  if (const int ks = res_ks(a, lw, fast_ok)) return launch_res<KIND>(a, ks, stream);
   if (const int wm = wide_wm(a, lw)) {
     a.n_tiles = (int)cdiv((int64_t)a.Cout, (8 / wm) * 64);
     a.m_tiles = (int)cdiv((int64_t)a.M, wm * 80);
