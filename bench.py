@@ -32,7 +32,7 @@ PEAK_HBM_GBS = 8000.0
 # HBM bytes per launch of the config-2 conv from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs (KiB per dispatch), each
 # scaled by what the counter reads for a plain 64 MiB device copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); the runs and the
 # arithmetic are in profiles/conv_mxfp8_1x1_gelu_cfg2.md. Re-measured by hand when the kernel changes.
-CFG2_TRAFFIC_BYTES = int((6184.0 * 2.0 + 20000.0 * 1.0) * 1024)  # the op's one launch (whole-K pointwise kernel)
+CFG2_TRAFFIC_BYTES = int((6244.0 * 2.0 + 20000.0 * 1.0) * 1024)  # the op's one launch (whole-K pointwise kernel)
 # The config-4 block's algorithmic HBM bytes when fused (204.8 MB for 2 x 400 x 400 x 64: 10 bytes per
 # element); GBps_own_launches divides instead the bytes this library's own launches of the block must move once.
 CFG4_FUSED_BYTES = 204_800_000
@@ -40,7 +40,7 @@ CFG4_FUSED_BYTES = 204_800_000
 # --pmc runs (profiles/*.md), x 4 cycles per 64-lane instruction on a 16-lane SIMD / 1024 SIMDs / 2.4 GHz. These
 # kernels are bound by that floor before HBM or MFMA; re-measured by hand when a kernel changes.
 VALU_INSTS = {
-    "cfg2_mxfp8_1x1_gelu": 3.191e6,         # conv_1x1_resident_kernel (GELU epilogue)
+    "cfg2_mxfp8_1x1_gelu": 2.92e6,          # conv_1x1_resident_kernel (GELU epilogue)
     "cfg3_mxfp8_3x3_bn_relu": 2.542e6,       # conv_patch_kernel
     "cfg4_depthwise_gelu_mxfp8": 9.10e6,    # dw5x5_mfma_kernel<GELU, static MXFP8>
 }
