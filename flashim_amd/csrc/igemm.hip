@@ -1511,7 +1511,9 @@ __global__ __launch_bounds__(512, 1) void conv_patch_kernel(const ConvArgs a) {
         __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));  // the staged rows read before the next round overwrites them
       }
     });
-    if (next < total) wait_vm_at_most(SROUNDS * SCH);  // this wavefront's patch loads, issued before its stores
+    // this wavefront's patch loads landed before the phase barrier hands the patch to its group: a full vmcnt(0), as
+    // the stores issued after them may complete first (the counter makes no order between loads and stores)
+    if (next < total) __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
   };
 
   for (int ph = 0; ph < n_phases; ++ph) {
@@ -2130,11 +2132,11 @@ __global__ __launch_bounds__(512, 1) void conv_1x1_resident_kernel(const ConvArg
       for (int j = 0; j < MB; ++j) mrow[j] = (t / a.n_tiles) * BM + wm * (MB * 16) + j * 16 + (lane & 15);
       conv_epilogue_rows<KIND, OUT, MB, NB>(a, acc_i, acc_f, mrow, n0, wn * (NB * 16), ep_scale, ep_bias, ep_osc);
     }
-    // the next tile's activations landed: every wavefront issued exactly MB x NB stores (and, with a residual, as
-    // many loads) after the activation loads, so waiting for at most that many leaves its stores in flight. Also after
-    // the last tile (nothing to wait for then but the stores): unconditional, so that the compiler's own accounting
-    // sees this wait on every path into the next tile's LDS reads
-    wait_vm_at_most(MB * NB);
+    // the next tile's activations landed in every wavefront's chunks before any wavefront reads them. A full vmcnt(0):
+    // the epilogue's stores, issued after the activation loads, may complete before them (the counter makes no order
+    // between loads and stores), so no smaller count proves the loads done. Unconditional (also after the last tile),
+    // so that the compiler's own accounting sees this wait on every path into the next tile's LDS reads
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
     asm volatile("s_barrier" ::: "memory");
   };
   run_tile(first, std::true_type{});
