@@ -513,6 +513,8 @@ ROW_CASES = [
     ("k2_n144_resident", (2, 110, 111), 256, 144),
     ("k3_n256_resident", (1, 150, 151), 384, 256),
     ("k4_n512_resident", (2, 100, 101), 512, 512),
+    # a resident-sized shape whose Cout % 16 != 0 needs the general epilogue: it takes the other kernels
+    ("k2_n136_resident_size_general", (2, 110, 111), 256, 136),
     ("k1_partial_tile", (1, 7, 13), 128, 128),
     ("k2_n144", (2, 9, 11), 256, 144),
     ("k3_n256", (1, 30, 31), 384, 256),
